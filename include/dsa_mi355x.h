@@ -1,0 +1,132 @@
+/*
+ * C ABI of the MI355X (gfx950) DeepSeek-Sparse-Attention library, libdsa_mi355x.so.
+ *
+ * The reference (tilelang-ascend) generates, per kernel, a C entry point
+ *   extern "C" void call(uint8_t* p0, ..., uint8_t* pN, [int64 shape vars], aclrtStream stream)
+ * whose pointer parameters are the PrimFunc's tensors in order (inputs, outputs,
+ * workspaces) and which launches on the given stream
+ * (src/target/codegen_ascend.cc:1141-1156,1205-1226; a hand-written declaration of
+ * one such entry point is examples/torch_tl_ascend/src/_inner.cpp:8-15).
+ * The entry points below play that role for the three kernels of the DSA path.
+ * They differ from the reference's `call` in two deliberate ways:
+ *   - they return an int status (0 = success) and record a message readable
+ *     through dsa_last_error(), the convention of the reference's CUDA/HIP
+ *     wrappers (tilelang/jit/adapter/wrapper.py:29-41), where `call` is void;
+ *   - sizes are explicit int64 arguments rather than baked into the kernel.
+ * All pointers are device pointers (except where noted) to contiguous tensors;
+ * the library never allocates device memory: outputs and workspaces are the
+ * caller's, as with the reference's out_idx / workspace_idx tensors
+ * (tilelang/jit/adapter/cython/cython_wrapper.pyx:102-141).  `stream` is a
+ * hipStream_t (NULL = the default stream); every call is asynchronous.
+ */
+#ifndef DSA_MI355X_H_
+#define DSA_MI355X_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define DSA_OK 0
+#define DSA_E_INVALID_ARGUMENT 1
+#define DSA_E_WORKSPACE_TOO_SMALL 2
+#define DSA_E_UNSUPPORTED 3
+#define DSA_E_HIP 4
+
+/* Message describing this thread's last failed call ("" if none). */
+const char* dsa_last_error(void);
+void dsa_clear_error(void);
+int dsa_abi_version(void);
+
+/*
+ * Row-wise top-k of fp32 scores.
+ * Replaces the `call` generated for simple_topk_selector's PrimFunc
+ * main(x[B,N] fp32, indices[B,top_k] int32)
+ * (examples/topk_selector/example_topk_selector.py:19-54), and the sort/merge
+ * top-k stage inside the lightning indexer kernel
+ * (examples/deepseek_v4/lightning_indexer.py:945-1036,1116-1196).
+ *
+ * scores  [rows, ld] fp32, row r uses columns [0, min(row_len[r], cols)) (row_len
+ *         may be NULL = all cols).
+ * out_idx [rows, k] int32: argsort(-row, stable=True)[:k]; entries <= -1e30 become
+ *         -1 when pad_invalid != 0; positions past the row length are -1.
+ * out_val [rows, k] fp32 or NULL: the selected values (-inf past the row length).
+ * Limits: k <= 8192, cols < 2^31.
+ */
+int dsa_topk_f32(const float* scores, int64_t rows, int64_t cols, int64_t ld,
+                 const int32_t* row_len, int32_t k, int32_t pad_invalid, int32_t* out_idx,
+                 float* out_val, void* stream);
+
+/*
+ * Lightning-indexer logits, fp8 e4m3 q and k with a per-key fp32 scale.
+ * Replaces the Cube QK + ReLU and Vector weight/head-reduce/mask stages of the
+ * `call` built by make_lightning_indexer_kernel
+ * (examples/deepseek_v4/lightning_indexer.py:661-795,868-944; golden :303-314).
+ *
+ * q [B, S1, N1, D] fp8, k [B, S2, D] fp8 (one key head), key_scale [B, S2] fp32 or
+ * NULL (= 1), weights [B, S1, N1] fp32, act_q / act_k [B] int32 per-batch lengths or
+ * NULL (= S1 / S2).  sparse_mode 3 = right-down causal, 0 = none.  N1 = 64, D = 128.
+ * logits [B * S1, ld] fp32: entry (t, s) is written for s < row_len[t] (masked
+ * entries inside computed tiles are -inf; others are left untouched).
+ * row_len [B * S1] int32 or NULL: number of keys row t attends to.
+ */
+int dsa_indexer_logits_fp8(const void* q, const void* k, const float* key_scale,
+                           const float* weights, const int32_t* act_q, const int32_t* act_k,
+                           int64_t B, int64_t S1, int64_t S2, int32_t N1, int32_t D,
+                           int32_t sparse_mode, float* logits, int64_t ld, int32_t* row_len,
+                           void* stream);
+
+/*
+ * Full lightning indexer: logits (above) then top-`sparse_count` per query row.
+ * Replaces the whole `call` of make_lightning_indexer_kernel
+ * (examples/deepseek_v4/lightning_indexer.py:338-1199) behind the host wrapper
+ * lightning_indexer (:1202-1376) for the BSND layout with N2 = 1.
+ * indices [B, S1, sparse_count] int32, values [B, S1, sparse_count] fp32 or NULL.
+ * workspace: dsa_lightning_indexer_workspace_bytes(B, S1, S2) bytes.
+ */
+size_t dsa_lightning_indexer_workspace_bytes(int64_t B, int64_t S1, int64_t S2);
+int dsa_lightning_indexer_fp8(const void* q, const void* k, const float* key_scale,
+                              const float* weights, const int32_t* act_q, const int32_t* act_k,
+                              int64_t B, int64_t S1, int64_t S2, int32_t N1, int32_t D,
+                              int32_t sparse_count, int32_t sparse_mode, int32_t* indices,
+                              float* values, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/*
+ * Sparse MLA forward: bf16 q [B, S, H, d_qk], one latent KV head, d_v = 512.
+ * Replaces the `call` of sparse_attention_fwd
+ * (examples/sparse_flash_attention/example_sparse_flash_attn.py:18-243, main(Q, KV,
+ * Indices, Output, workspace_1..5)) and of the paged variant
+ * (examples/sparse_flash_attention/bench_sfa/sparse_flash_attn_pa_no_cv_pipeline.py:27-377),
+ * and adds the LSE output of the DeepSeek-V4 sparse flash MLA
+ * (examples/deepseek_v4/sparse_flash_mla/sparse_flash_mla_kernel.py:2120-2131).
+ *
+ * kv: contiguous [B, skv, 1, d_qk] bf16 when block_table is NULL, else a page pool
+ *     [num_blocks, block_size, 1, d_qk] addressed through block_table [B, max_blocks];
+ *     then skv = num_blocks * block_size (pages outside the pool are skipped).
+ * indices [B, S, 1, topk] int32; entries < 0, >= kv_len[b] (NULL: skv or
+ *     max_blocks*block_size), on a page < 0, or (is_causal) > q_start[b] + s
+ *     (q_start NULL: kv_len[b] - S) are skipped.
+ * attn_sink [H] fp32 or NULL.  d_qk in {576, 512}.
+ * out [B, S, H, 512] bf16, lse [B, S, H] fp32 (natural log) or NULL.
+ * num_splits: index-list splits per token (0 = automatic); with more than one
+ *     split the workspace must hold dsa_sparse_mla_workspace_bytes(...) bytes.
+ */
+size_t dsa_sparse_mla_workspace_bytes(int64_t B, int64_t S, int32_t H, int32_t topk,
+                                      int32_t num_splits);
+int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices,
+                       const int32_t* block_table, const int32_t* kv_len, const int32_t* q_start,
+                       const float* attn_sink, int64_t B, int64_t S, int32_t H, int32_t d_qk,
+                       int32_t d_v, int64_t skv, int32_t block_size, int32_t max_blocks,
+                       int32_t topk, float sm_scale, int32_t is_causal, int32_t num_splits,
+                       void* out, float* lse, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_MI355X_H_ */

@@ -1,0 +1,89 @@
+"""GPU parity of the sparse-MLA kernel against the oracle.
+
+Tolerances: out within bf16 atol = rtol = 2e-2, LSE
+within 1e-3 (absolute and relative).  The oracle rounds the probabilities to bf16
+before the PV product as sparse_flash_mla_golden.py:143 does."""
+import pytest
+import torch
+
+import dsa
+from dsa import inputs
+from oracle.dsa_oracle import sparse_mla_fwd_gather
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL = dict(rtol=2e-2, atol=2e-2)
+LSE_TOL = dict(rtol=1e-3, atol=1e-3)
+
+
+def _check(inp, gpu, **kw):
+    q, kv, idx = inp["q"], inp["kv"], inp["indices"]
+    print(f"mla case q={tuple(q.shape)} kv={tuple(kv.shape)} topk={idx.shape[-1]} kw={kw}", flush=True)
+    out, lse = dsa.sparse_mla_fwd(q.to(gpu), kv.to(gpu), idx.to(gpu), inp.get("sm_scale"),
+                                  **{k: (v.to(gpu) if torch.is_tensor(v) else v) for k, v in kw.items()})
+    torch.cuda.synchronize()
+    ref_kw = {k: v for k, v in kw.items() if k in ("block_table", "q_start_index_s", "is_causal", "attn_sink")}
+    if "seq_len_kv" in kw:
+        pass  # every index in these cases is below seq_len_kv
+    ro, rl = sparse_mla_fwd_gather(q, kv, idx, inp.get("sm_scale"), p_dtype=torch.bfloat16, **ref_kw)
+    torch.testing.assert_close(out.float().cpu(), ro, **OUT_TOL)
+    torch.testing.assert_close(lse.cpu(), rl, **LSE_TOL)
+    return out.cpu(), lse.cpu()
+
+
+def test_config1_small(gpu):
+    inp = inputs.mla_prefill()  # config 1: B=1 S=128 Skv=4096 H=16 topk=512
+    _check(inp, gpu, is_causal=True)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 8])
+def test_splits_agree(gpu, splits):
+    inp = inputs.mla_prefill(B=2, S=8, Skv=2048, H=128, topk=1024, seed=11)
+    _check(inp, gpu, num_splits=splits)
+
+
+def test_minus_one_padding_and_sentinel(gpu):
+    inp = inputs.mla_prefill(B=1, S=64, Skv=64, H=32, topk=128, seed=12, q_start=0)
+    idx = inp["indices"]
+    assert (idx == -1).any()
+    idx[0, 5, 0, 0] = 64          # out-of-range sentinel Skv
+    idx[0, 6, 0, :] = -1          # a row with nothing to attend to
+    out, lse = _check(inp, gpu, is_causal=True)
+    assert torch.count_nonzero(out[0, 6]) == 0 and torch.isinf(lse[0, 6]).all()
+
+
+def test_causal_mask_applies(gpu):
+    inp = inputs.mla_prefill(B=1, S=16, Skv=512, H=16, topk=64, seed=13)
+    g = torch.Generator().manual_seed(0)
+    inp["indices"] = torch.randint(0, 512, (1, 16, 1, 64), generator=g, dtype=torch.int32)
+    _check(inp, gpu, is_causal=True, q_start_index_s=100)
+    _check(inp, gpu, is_causal=False)
+
+
+def test_paged_decode_small(gpu):
+    inp = inputs.mla_decode(B=4, ctx=4096, H=128, topk=512, block_size=64, seed=14)
+    _check(inp, gpu, block_table=inp["block_table"], seq_len_kv=inp["seq_len_kv"], is_causal=False)
+
+
+def test_d512_with_sink(gpu):
+    inp = inputs.mla_prefill(B=1, S=16, Skv=256, H=64, topk=128, seed=15, d_qk=512)
+    g = torch.Generator().manual_seed(1)
+    sink = torch.randn(64, generator=g)
+    _check(inp, gpu, attn_sink=sink, is_causal=False)
+
+
+def test_head_count_not_multiple_of_16(gpu):
+    inp = inputs.mla_prefill(B=1, S=4, Skv=300, H=20, topk=96, seed=16)
+    _check(inp, gpu)
+
+
+def test_reference_factory_fp16_sentinel_convention(gpu):
+    # sparse_attention_fwd pads indices with the sentinel Skv (example_sparse_flash_attn.py:303)
+    inp = inputs.mla_prefill(B=1, S=32, Skv=1024, H=128, topk=256, seed=17, q_start=900)
+    idx = inp["indices"].clone()
+    idx[idx < 0] = 1024
+    kern = dsa.sparse_attention_fwd(heads=128, dim=512, tail_dim=64, topk=256, kv_stride=1)
+    out = kern(inp["q"].to(gpu), inp["kv"].to(gpu), idx.to(gpu)).float().cpu()
+    ro, _ = sparse_mla_fwd_gather(inp["q"], inp["kv"], inp["indices"], None, q_start_index_s=900,
+                                  is_causal=True, p_dtype=torch.bfloat16)
+    torch.testing.assert_close(out, ro, **OUT_TOL)

@@ -1,0 +1,345 @@
+"""Python entry points of the MI355X DSA path, with the reference's call signatures.
+
+Each function validates its arguments the way the reference's host wrapper does
+(same conditions, ``ValueError``/``AssertionError`` where the reference raises
+them), allocates outputs and workspaces with torch on the input's device (the
+reference's ``out_idx`` / ``workspace_idx`` convention,
+tilelang/jit/adapter/cython/cython_wrapper.pyx:102-141) and calls the HIP library
+through its C ABI on the current stream.  There is no CPU path: tensors must be
+on a ROCm device and the library must be built.
+"""
+
+from __future__ import annotations
+
+from typing import Callable, Optional, Tuple
+
+import torch
+
+from ._lib import check, lib
+
+INT64_MAX = (1 << 63) - 1
+_FP8 = getattr(torch, "float8_e4m3fn", None)
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(f"expected a tensor on a ROCm device, got one on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors are on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _require_contiguous(name: str, t: torch.Tensor) -> None:
+    # cython_wrapper.pyx:148-150 raises for non-contiguous inputs
+    if not t.is_contiguous():
+        raise ValueError(f"Expected {name} to be contiguous")
+
+
+def _int32_vec(name: str, t: Optional[torch.Tensor], n: int, device) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    t = torch.as_tensor(t)
+    if t.numel() != n:
+        raise ValueError(f"{name} must have {n} entries, got {t.numel()}")
+    return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# top-k selector
+# ---------------------------------------------------------------------------
+def topk_selector(x: torch.Tensor, top_k: int, *, row_len: Optional[torch.Tensor] = None,
+                  pad_invalid: bool = True, return_values: bool = False):
+    """Row-wise top-k of fp32 ``x [B, N]`` -> int32 indices ``[B, top_k]``.
+
+    Same output as the topk_selector example's reference ``torch.topk(x, k)[1]``
+    (examples/topk_selector/example_topk_selector.py:57-58) with the ordering and
+    tie rule of the lightning-indexer golden: descending value, equal values in
+    ascending index order (examples/deepseek_v4/lightning_indexer.py:318-320).
+    With ``pad_invalid`` entries whose value is <= -1e30 (masked) become -1, and
+    rows shorter than ``top_k`` (``row_len``) are padded with -1 (:321-325).
+    """
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2-D [B, N], got shape {tuple(x.shape)}")
+    if x.dtype != torch.float32:
+        raise ValueError(f"x must be float32, got {x.dtype}")
+    dev = _require_gpu(x, row_len)
+    _require_contiguous("x", x)
+    B, N = x.shape
+    if not (1 <= top_k <= 8192):
+        raise ValueError(f"top_k must be in [1, 8192], got {top_k}")
+    rl = _int32_vec("row_len", row_len, B, dev)
+    idx = torch.empty((B, top_k), dtype=torch.int32, device=dev)
+    val = torch.empty((B, top_k), dtype=torch.float32, device=dev) if return_values else None
+    check(lib().dsa_topk_f32(_ptr(x), B, N, N, _ptr(rl), top_k, int(bool(pad_invalid)), _ptr(idx),
+                             _ptr(val), _stream(dev)), "dsa_topk_f32")
+    return (idx, val) if return_values else idx
+
+
+def simple_topk_selector(B: int, N: int, top_k: int, block_N: int, dtype: str = "float32") -> Callable:
+    """Factory with the signature of the reference's JIT kernel builder
+    (examples/topk_selector/example_topk_selector.py:19): returns ``kernel(x) -> indices``.
+    ``block_N`` was the reference's UB copy granularity and has no effect here."""
+    if dtype != "float32":
+        raise ValueError(f"simple_topk_selector supports float32 only, got {dtype}")
+    del block_N
+
+    def kernel(x: torch.Tensor) -> torch.Tensor:
+        if tuple(x.shape) != (B, N):
+            raise ValueError(f"expected x of shape {(B, N)}, got {tuple(x.shape)}")
+        return topk_selector(x, top_k, pad_invalid=False)
+
+    return kernel
+
+
+# ---------------------------------------------------------------------------
+# lightning indexer
+# ---------------------------------------------------------------------------
+def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Tensor, *,
+                      key_scale: Optional[torch.Tensor] = None,
+                      actual_seq_lengths_query: Optional[torch.Tensor] = None,
+                      actual_seq_lengths_key: Optional[torch.Tensor] = None,
+                      block_table: Optional[torch.Tensor] = None,
+                      layout_query: str = "BSND", layout_key: str = "BSND",
+                      sparse_count: int = 2048, sparse_mode: int = 3,
+                      pre_tokens: int = INT64_MAX, next_tokens: int = INT64_MAX,
+                      return_value: bool = False, block_n: Optional[int] = None,
+                      pp_slots: int = 2, max_cores: Optional[int] = None,
+                      return_logits: bool = False):
+    """Lightning indexer: per query row the ``sparse_count`` keys with the largest
+    ``sum_h w[h] * ReLU(q[h] . k)`` (times ``key_scale``), causal for sparse_mode 3.
+
+    Signature and validation of ``lightning_indexer``
+    (examples/deepseek_v4/lightning_indexer.py:1202-1283); semantics of its golden
+    ``cpu_lightning_indexer`` (:199-335).  Differences: q/k are fp8 e4m3
+    (``torch.float8_e4m3fn``) with an optional per-key fp32 ``key_scale`` of shape
+    ``[B, S2]`` (or ``[B, S2, 1]``); returned ``values`` are fp32.  ``block_n``,
+    ``pp_slots`` and ``max_cores`` were Ascend tiling knobs and are accepted and
+    ignored.  Layouts: BSND query and key with N2 = 1.
+    Returns ``(indices int32 [B, S1, 1, sparse_count], values)``; ``values`` is an
+    empty tensor unless ``return_value``.  ``return_logits`` additionally returns
+    the fp32 logits ``[B, S1, S2]`` (valid for keys < the row's causal length).
+    """
+    del block_n, pp_slots, max_cores
+    if layout_query not in ("BSND", "TND"):
+        raise AssertionError(f"Unsupported query layout: {layout_query}")
+    if layout_key not in ("BSND", "PA_BSND", "TND"):
+        raise AssertionError(f"Unsupported key layout: {layout_key}")
+    is_pa = layout_key == "PA_BSND"
+    if is_pa and return_value:
+        raise ValueError("PA_BSND layout does not support return_value")
+    if not is_pa and layout_query != layout_key:
+        raise ValueError(f"layout_query({layout_query}) must equal layout_key({layout_key}) when key is non-PA_BSND")
+    if not (1 <= sparse_count <= 2048 or (sparse_count % 1024 == 0 and sparse_count <= 8192)):
+        raise ValueError(f"sparse_count must be in [1,2048] or a multiple of 1024 up to 8192, got {sparse_count}")
+    if sparse_mode not in (0, 3):
+        raise ValueError(f"sparse_mode must be 0 (defaultMask) or 3 (rightDownCausal), got {sparse_mode}")
+    if pre_tokens != INT64_MAX:
+        raise ValueError(f"pre_tokens must be INT64_MAX, got {pre_tokens}")
+    if next_tokens != INT64_MAX:
+        raise ValueError(f"next_tokens must be INT64_MAX, got {next_tokens}")
+    if query.dtype != key.dtype:
+        raise ValueError(f"query dtype {query.dtype} must equal key dtype {key.dtype}")
+    if query.dtype != _FP8:
+        raise ValueError(f"query/key dtype must be float8_e4m3fn, got {query.dtype}")
+    if weights.dtype != torch.float32:
+        raise ValueError(f"weights dtype {weights.dtype} must be float32")
+    if layout_query != "BSND" or layout_key != "BSND" or block_table is not None:
+        raise NotImplementedError("only the BSND query/key layout is built")
+    if query.dim() != 4 or key.dim() != 4:
+        raise ValueError("BSND query and key must be 4-D [B, S, N, D]")
+    B, S1, N1, D = query.shape
+    Bk, S2, N2, Dk = key.shape
+    if Bk != B or Dk != D:
+        raise ValueError(f"key shape {tuple(key.shape)} does not match query {tuple(query.shape)}")
+    if D != 128:
+        raise AssertionError(f"head dim must be 128, got {D}")
+    if N2 != 1:
+        raise AssertionError(f"N2 must be 1, got N2={N2}")
+    if N1 > 64:
+        raise ValueError(f"query head_num (N1) must be <= 64, got {N1}")
+    if N1 != 64:
+        raise NotImplementedError(f"the fp8 kernel is built for N1 = 64 index heads, got {N1}")
+    if tuple(weights.shape) != (B, S1, N1):
+        raise ValueError(f"weights must be [B, S1, N1] = {(B, S1, N1)}, got {tuple(weights.shape)}")
+    dev = _require_gpu(query, key, weights, key_scale)
+    for name, t in (("query", query), ("key", key), ("weights", weights)):
+        _require_contiguous(name, t)
+    ks = None
+    if key_scale is not None:
+        if key_scale.numel() != B * S2:
+            raise ValueError(f"key_scale must have B*S2 = {B * S2} entries, got {key_scale.numel()}")
+        ks = key_scale.to(torch.float32).contiguous()
+    aq = _int32_vec("actual_seq_lengths_query", actual_seq_lengths_query, B, dev)
+    ak = _int32_vec("actual_seq_lengths_key", actual_seq_lengths_key, B, dev)
+
+    indices = torch.empty((B, S1, 1, sparse_count), dtype=torch.int32, device=dev)
+    values = (torch.empty((B, S1, 1, sparse_count), dtype=torch.float32, device=dev)
+              if return_value else None)
+    L = lib()
+    ws_bytes = L.dsa_lightning_indexer_workspace_bytes(B, S1, S2)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    check(L.dsa_lightning_indexer_fp8(_ptr(query), _ptr(key), _ptr(ks), _ptr(weights), _ptr(aq), _ptr(ak),
+                                      B, S1, S2, N1, D, sparse_count, sparse_mode, _ptr(indices),
+                                      _ptr(values), _ptr(ws), ws_bytes, _stream(dev)),
+          "dsa_lightning_indexer_fp8")
+    if values is None:
+        values = torch.empty((0,), dtype=torch.float32, device=dev)
+    if return_logits:
+        logits = ws[: B * S1 * S2 * 4].view(torch.float32).view(B, S1, S2)
+        return indices, values, logits
+    return indices, values
+
+
+def indexer_logits(query: torch.Tensor, key: torch.Tensor, weights: torch.Tensor, *,
+                   key_scale: Optional[torch.Tensor] = None,
+                   actual_seq_lengths_query: Optional[torch.Tensor] = None,
+                   actual_seq_lengths_key: Optional[torch.Tensor] = None,
+                   sparse_mode: int = 3) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The logits stage alone: ``(logits fp32 [B, S1, S2], row_len int32 [B, S1])``.
+    ``logits[b, t, s]`` is defined for ``s < row_len[b, t]`` (the golden's
+    ``full_scores`` there, lightning_indexer.py:303-314)."""
+    B, S1, N1, D = query.shape
+    S2 = key.shape[1]
+    if query.dtype != _FP8 or key.dtype != _FP8:
+        raise ValueError("query/key must be float8_e4m3fn")
+    dev = _require_gpu(query, key, weights, key_scale)
+    for name, t in (("query", query), ("key", key), ("weights", weights)):
+        _require_contiguous(name, t)
+    ks = None if key_scale is None else key_scale.to(torch.float32).contiguous()
+    aq = _int32_vec("actual_seq_lengths_query", actual_seq_lengths_query, B, dev)
+    ak = _int32_vec("actual_seq_lengths_key", actual_seq_lengths_key, B, dev)
+    logits = torch.empty((B, S1, S2), dtype=torch.float32, device=dev)
+    row_len = torch.zeros((B, S1), dtype=torch.int32, device=dev)
+    check(lib().dsa_indexer_logits_fp8(_ptr(query), _ptr(key), _ptr(ks), _ptr(weights), _ptr(aq), _ptr(ak),
+                                       B, S1, S2, N1, D, sparse_mode, _ptr(logits), S2, _ptr(row_len),
+                                       _stream(dev)), "dsa_indexer_logits_fp8")
+    return logits, row_len
+
+
+# ---------------------------------------------------------------------------
+# sparse MLA forward
+# ---------------------------------------------------------------------------
+def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor,
+                   sm_scale: Optional[float] = None, *, d_v: int = 512,
+                   block_table: Optional[torch.Tensor] = None,
+                   seq_len_kv: Optional[torch.Tensor] = None,
+                   q_start_index_s=None, is_causal: bool = True,
+                   attn_sink: Optional[torch.Tensor] = None,
+                   num_splits: int = 0, return_lse: bool = True):
+    """Sparse MLA forward with one shared latent KV head -> ``(out, lse)``.
+
+    q ``[B, S, H, d_qk]`` bf16 (d_qk 576 = 512 latent + 64 rope, or 512);
+    kv ``[B, Skv, 1, d_qk]`` bf16, or a page pool ``[blocks, block_size, 1, d_qk]``
+    with ``block_table [B, max_blocks]`` int32 (index i of batch b lives at
+    ``pool[block_table[b, i // block_size], i % block_size]``,
+    bench_sfa/sparse_flash_attn_pa_no_cv_pipeline.py:196-200); indices
+    ``[B, S, 1, topk]`` int32.  Semantics follow ``sparse_attention_fwd`` and its
+    reference (examples/sparse_flash_attention/example_sparse_flash_attn.py:18-292)
+    with the gather rule of examples/deepseek_v4/sparse_attention.py:171-198:
+    ``-1`` and out-of-range indices are skipped; ``is_causal`` also skips indices
+    above ``q_start_index_s + s`` (default ``Skv - S``; per batch if a tensor).
+    ``out [B, S, H, 512]`` bf16 and ``lse [B, S, H]`` fp32 (natural log,
+    sparse_flash_mla_golden.py:147-149).  A row without a valid index gets
+    out = 0 and lse = -inf.
+    """
+    if q.dtype != torch.bfloat16 or kv.dtype != torch.bfloat16:
+        raise ValueError(f"q and kv must be bfloat16, got {q.dtype} and {kv.dtype}")
+    if indices.dtype != torch.int32:
+        raise ValueError(f"indices must be int32, got {indices.dtype}")
+    if q.dim() != 4 or kv.dim() != 4 or indices.dim() != 4:
+        raise ValueError("q, kv and indices must be 4-D")
+    B, S, H, d_qk = q.shape
+    if d_v != 512:
+        raise ValueError(f"d_v must be 512, got {d_v}")
+    if d_qk not in (576, 512):
+        raise ValueError(f"d_qk must be 576 or 512, got {d_qk}")
+    if kv.shape[2] != 1 or kv.shape[3] != d_qk:
+        raise ValueError(f"kv must be [*, *, 1, {d_qk}], got {tuple(kv.shape)}")
+    if indices.shape[0] != B or indices.shape[1] != S or indices.shape[2] != 1:
+        raise ValueError(f"indices must be [B, S, 1, topk] = [{B}, {S}, 1, topk], got {tuple(indices.shape)}")
+    topk = indices.shape[3]
+    dev = _require_gpu(q, kv, indices, block_table, attn_sink)
+    for name, t in (("q", q), ("kv", kv), ("indices", indices)):
+        _require_contiguous(name, t)
+    paged = block_table is not None
+    if paged:
+        if block_table.dim() != 2 or block_table.shape[0] != B:
+            raise ValueError(f"block_table must be [B, max_blocks], got {tuple(block_table.shape)}")
+        bt = block_table.to(torch.int32).contiguous()
+        block_size = kv.shape[1]
+        max_blocks = bt.shape[1]
+        skv = kv.shape[0] * block_size  # rows in the pool
+    else:
+        if kv.shape[0] != B:
+            raise ValueError(f"kv batch {kv.shape[0]} != q batch {B}")
+        bt = None
+        block_size = max_blocks = 0
+        skv = kv.shape[1]
+    kvl = _int32_vec("seq_len_kv", seq_len_kv, B, dev)
+    qs = None
+    if q_start_index_s is not None:
+        if isinstance(q_start_index_s, int):
+            qs = torch.full((B,), q_start_index_s, dtype=torch.int32, device=dev)
+        else:
+            qs = _int32_vec("q_start_index_s", q_start_index_s, B, dev)
+    sink = None
+    if attn_sink is not None:
+        if attn_sink.numel() != H:
+            raise ValueError(f"attn_sink must have H = {H} entries")
+        sink = attn_sink.to(torch.float32).contiguous()
+    if sm_scale is None:
+        sm_scale = d_qk ** -0.5
+    out = torch.empty((B, S, H, d_v), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, S, H), dtype=torch.float32, device=dev)
+    L = lib()
+    ws_bytes = L.dsa_sparse_mla_workspace_bytes(B, S, H, topk, num_splits)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    check(L.dsa_sparse_mla_fwd(_ptr(q), _ptr(kv), _ptr(indices), _ptr(bt), _ptr(kvl), _ptr(qs), _ptr(sink),
+                               B, S, H, d_qk, d_v, skv, block_size, max_blocks, topk, float(sm_scale),
+                               int(bool(is_causal)), int(num_splits), _ptr(out), _ptr(lse), _ptr(ws),
+                               ws_bytes, _stream(dev)), "dsa_sparse_mla_fwd")
+    return (out, lse) if return_lse else out
+
+
+def sparse_attention_fwd(heads: int, dim: int, tail_dim: int, topk: int, kv_stride: int,
+                         kv_group: int = 1, sm_scale: Optional[float] = None, is_causal: bool = True,
+                         block_I: int = 64) -> Callable:
+    """Factory with the signature of the reference's ``sparse_attention_fwd``
+    (examples/sparse_flash_attention/example_sparse_flash_attn.py:18-46), returning
+    ``kernel(q, kv, indices) -> out``.  Asserts as the reference does; the
+    out-of-range sentinel ``Skv`` used to pad its indices (:303) is skipped."""
+    def _pow2(x):
+        return x > 0 and (x & (x - 1)) == 0
+    assert _pow2(dim), f"haven't check padding correctness yet, dim={dim}"
+    assert _pow2(tail_dim), f"haven't check padding correctness yet, dim={tail_dim}"
+    assert is_causal, "non-casual is not supported"
+    assert topk % block_I == 0, "otherwise will load some index=0 thus causing wrong kv to be loaded"
+    if kv_group != 1:
+        raise NotImplementedError("one latent KV head (kv_group = 1) only")
+    if kv_stride != 1:
+        raise NotImplementedError("kv_stride = 1 only")
+    scale = (1.0 / (dim + tail_dim)) ** 0.5 if sm_scale is None else sm_scale
+
+    def kernel(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        if q.shape[2] != heads or q.shape[3] != dim + tail_dim or indices.shape[3] != topk:
+            raise ValueError("q / indices shape does not match the kernel's heads, dim + tail_dim, topk")
+        return sparse_mla_fwd(q, kv, indices, scale, is_causal=is_causal, return_lse=False)
+
+    return kernel
