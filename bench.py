@@ -1,0 +1,278 @@
+"""Benchmark of the MI355X DSA path (one GPU).
+
+Default workload = the full DSA layer at 128K context:
+  prefill chunk: lightning indexer (fp8, 64 heads x 128) of 4096 tail queries over
+                 131072 keys -> top-2048 -> sparse MLA (H=128, d_qk=576, d_v=512) on
+                 the chunk with those indices;
+  decode step:   32 single-token queries at position 131072 over the same cache
+                 (32 block tables on one 64-token page pool) through all three kernels.
+One step = both.  Inputs are synthetic (seeded), resident in HBM before timing.
+Prints one JSON line.  ``value`` = sparse-MLA TFLOP/s of the prefill chunk
+(2*H*topk*(576+512) FLOP per token / MLA kernel time); the indexer / top-k times
+per call are reported beside it.  ``roofline`` is for the kernel with the largest
+share of the step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "tilelang-ascend_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP8_TFLOPS = 5000.0
+PEAK_HBM_GBS = 8000.0
+METRIC = "sparse-MLA TFLOPS (% MFMA peak) + indexer/top-k µs @H=128, topk=2048"
+
+H, DQK, DV, TOPK, IDX_HEADS, IDX_DIM = 128, 576, 512, 2048, 64, 128
+
+
+def mla_flops(tokens: int) -> float:
+    return 2.0 * H * TOPK * (DQK + DV) * tokens
+
+
+def indexer_flops_causal(S1: int, S2: int) -> float:
+    # valid (query, key) pairs under the right-down causal mask, 2*64*128 FLOP each
+    pairs = sum(S2 - S1 + t + 1 for t in range(S1))
+    return 2.0 * IDX_HEADS * IDX_DIM * pairs
+
+
+class Layer:
+    """Preallocated buffers and C-ABI launches for one DSA layer step."""
+
+    def __init__(self, S1: int, S2: int, dec_b: int, seed: int = 5):
+        import torch
+        from dsa import inputs, lib
+
+        self.torch = torch
+        self.L = lib()
+        dev = torch.device("cuda:0")
+        self.dev = dev
+        self.S1, self.S2, self.dec_b = S1, S2, dec_b
+        ix = inputs.indexer_fp8(B=1, S1=S1, S2=S2, seed=seed, device=dev)
+        self.iq, self.ik, self.iw, self.iks = ix["q"], ix["k"], ix["w"], ix["key_scale"]
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed + 100)
+        self.q = (torch.randn((1, S1, H, DQK), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+        self.kv = (torch.randn((1, S2, 1, DQK), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+        self.logits = torch.empty((S1, S2), dtype=torch.float32, device=dev)
+        self.row_len = torch.empty((S1,), dtype=torch.int32, device=dev)
+        self.idx = torch.empty((1, S1, 1, TOPK), dtype=torch.int32, device=dev)
+        self.out = torch.empty((1, S1, H, DV), dtype=torch.bfloat16, device=dev)
+        self.lse = torch.empty((1, S1, H), dtype=torch.float32, device=dev)
+        self.q_start = torch.full((1,), S2 - S1, dtype=torch.int32, device=dev)
+        # decode: dec_b queries at position S2 over the same cache, paged (64-token pages)
+        self.bs = 64
+        self.pool = self.kv.view(S2 // self.bs, self.bs, 1, DQK)
+        self.bt = torch.arange(S2 // self.bs, dtype=torch.int32, device=dev).repeat(dec_b, 1).contiguous()
+        self.dq_idx = torch.randn((1, dec_b, IDX_HEADS, IDX_DIM), generator=g, device=dev).to(inputs.FP8)
+        self.dw = torch.randn((1, dec_b, IDX_HEADS), generator=g, device=dev) / 8
+        self.dlogits = torch.empty((dec_b, S2), dtype=torch.float32, device=dev)
+        self.drow = torch.empty((dec_b,), dtype=torch.int32, device=dev)
+        self.didx = torch.empty((dec_b, 1, 1, TOPK), dtype=torch.int32, device=dev)
+        self.dq = (torch.randn((dec_b, 1, H, DQK), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+        self.dout = torch.empty((dec_b, 1, H, DV), dtype=torch.bfloat16, device=dev)
+        self.dlse = torch.empty((dec_b, 1, H), dtype=torch.float32, device=dev)
+        self.dlen = torch.full((dec_b,), S2, dtype=torch.int32, device=dev)
+        self.mla_ws_bytes = self.L.dsa_sparse_mla_workspace_bytes(1, S1, H, TOPK, 0)
+        self.dec_ws_bytes = self.L.dsa_sparse_mla_workspace_bytes(dec_b, 1, H, TOPK, 0)
+        self.ws = torch.empty((max(self.mla_ws_bytes, self.dec_ws_bytes, 1),), dtype=torch.uint8, device=dev)
+        self.names = ["indexer", "topk", "mla", "dec_indexer", "dec_topk", "dec_mla"]
+        self.stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def _chk(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: {self.L.dsa_last_error().decode()}")
+
+    def launch(self, i: int):
+        L, st = self.L, self.stream
+        if i == 0:
+            self._chk(L.dsa_indexer_logits_fp8(self.iq.data_ptr(), self.ik.data_ptr(), self.iks.data_ptr(),
+                                               self.iw.data_ptr(), None, None, 1, self.S1, self.S2, IDX_HEADS,
+                                               IDX_DIM, 3, self.logits.data_ptr(), self.S2,
+                                               self.row_len.data_ptr(), st), "indexer")
+        elif i == 1:
+            self._chk(L.dsa_topk_f32(self.logits.data_ptr(), self.S1, self.S2, self.S2, self.row_len.data_ptr(),
+                                     TOPK, 1, self.idx.data_ptr(), None, st), "topk")
+        elif i == 2:
+            self._chk(L.dsa_sparse_mla_fwd(self.q.data_ptr(), self.kv.data_ptr(), self.idx.data_ptr(), None, None,
+                                           self.q_start.data_ptr(), None, 1, self.S1, H, DQK, DV, self.S2, 0, 0,
+                                           TOPK, DQK ** -0.5, 1, 0, self.out.data_ptr(), self.lse.data_ptr(),
+                                           self.ws.data_ptr(), self.ws.numel(), st), "mla")
+        elif i == 3:
+            self._chk(L.dsa_indexer_logits_fp8(self.dq_idx.data_ptr(), self.ik.data_ptr(), self.iks.data_ptr(),
+                                               self.dw.data_ptr(), None, None, 1, self.dec_b, self.S2, IDX_HEADS,
+                                               IDX_DIM, 0, self.dlogits.data_ptr(), self.S2,
+                                               self.drow.data_ptr(), st), "dec_indexer")
+        elif i == 4:
+            self._chk(L.dsa_topk_f32(self.dlogits.data_ptr(), self.dec_b, self.S2, self.S2, self.drow.data_ptr(),
+                                     TOPK, 1, self.didx.data_ptr(), None, st), "dec_topk")
+        elif i == 5:
+            self._chk(L.dsa_sparse_mla_fwd(self.dq.data_ptr(), self.pool.data_ptr(), self.didx.data_ptr(),
+                                           self.bt.data_ptr(), self.dlen.data_ptr(), None, None, self.dec_b, 1, H,
+                                           DQK, DV, self.S2, self.bs, self.bt.shape[1], TOPK, DQK ** -0.5, 1, 0,
+                                           self.dout.data_ptr(), self.dlse.data_ptr(), self.ws.data_ptr(),
+                                           self.ws.numel(), st), "dec_mla")
+
+    def step(self, events=None):
+        for i in range(len(self.names)):
+            if events is not None:
+                events[i][0].record()
+            self.launch(i)
+            if events is not None:
+                events[i][1].record()
+
+
+def cpu_baseline(S1: int, S2: int, budget_rows: int = 32, mla_tokens: int = 96) -> dict:
+    """Time the CPU oracle on a bounded sample of the same workload and scale it."""
+    import torch
+
+    from dsa import inputs
+    from oracle.dsa_oracle import indexer_scores, sparse_mla_fwd_gather, stable_topk
+
+    threads = torch.get_num_threads()
+    ix = inputs.indexer_fp8(B=1, S1=budget_rows, S2=S2, seed=5)
+    k = ix["k"][0, :, 0].float() * ix["key_scale"][0].unsqueeze(1)
+    t0 = time.perf_counter()
+    # the sample rows are the last ones of the chunk: they see (almost) all keys
+    sc = indexer_scores(ix["q"][0].float(), k, ix["w"][0], budget_rows, S2, 3)
+    t1 = time.perf_counter()
+    stable_topk(sc, TOPK)
+    t2 = time.perf_counter()
+    g = torch.Generator().manual_seed(5)
+    q = (torch.randn((1, mla_tokens, H, DQK), generator=g) * 0.5).to(torch.bfloat16)
+    kv = (torch.randn((1, S2, 1, DQK), generator=g) * 0.5).to(torch.bfloat16)
+    idx = torch.stack([torch.randperm(S2 - S1, generator=g)[:TOPK] for _ in range(mla_tokens)]).int()
+    t3 = time.perf_counter()
+    sparse_mla_fwd_gather(q, kv, idx.view(1, mla_tokens, 1, TOPK), None, is_causal=False,
+                          p_dtype=torch.bfloat16)
+    t4 = time.perf_counter()
+    scale_rows = S1 / budget_rows
+    return {
+        "value": mla_flops(mla_tokens) / (t4 - t3) / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle (torch CPU): indexer+top-k on {budget_rows} of {S1} query rows x {S2} keys, "
+                   f"sparse MLA on {mla_tokens} of {S1} tokens; value = MLA TFLOP/s on the sample"),
+        "indexer_topk_us_scaled": (t2 - t0) * scale_rows * 1e6,
+        "mla_us_scaled": (t4 - t3) * (S1 / mla_tokens) * 1e6,
+        "cpu_model": _cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--s1", type=int, default=4096)
+    ap.add_argument("--s2", type=int, default=131072)
+    ap.add_argument("--dec-batch", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_indexer_layer128k.txt"),
+                    help="rocprofv3 --pmc summary holding the dominant kernel's HBM bytes per launch")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this path "
+              "(each GPU box has one GPU)", file=sys.stderr)
+        return 2
+    import torch
+
+    layer = Layer(args.s1, args.s2, args.dec_batch)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        layer.step()
+    torch.cuda.synchronize()
+    n = len(layer.names)
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        layer.step(evs[s])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = {name: 1e3 * sum(evs[s][i][0].elapsed_time(evs[s][i][1]) for s in range(args.steps)) / args.steps
+           for i, name in enumerate(layer.names)}  # microseconds per call
+    ms_per_step = wall * 1e3 / args.steps
+
+    S1, S2 = args.s1, args.s2
+    f_mla = mla_flops(S1)
+    f_idx = indexer_flops_causal(S1, S2)
+    mla_tflops = f_mla / (per["mla"] * 1e-6) / 1e12
+    idx_tflops = f_idx / (per["indexer"] * 1e-6) / 1e12
+    topk_bytes = 4.0 * sum(S2 - S1 + t + 1 for t in range(S1)) + 4.0 * S1 * TOPK
+    topk_gbs = topk_bytes / (per["topk"] * 1e-6) / 1e9
+
+    kern = {"indexer": ("mfma", idx_tflops, PEAK_FP8_TFLOPS, "TFLOP/s"),
+            "mla": ("mfma", mla_tflops, PEAK_BF16_TFLOPS, "TFLOP/s"),
+            "topk": ("hbm", topk_gbs, PEAK_HBM_GBS, "GB/s")}
+    dom = max(kern, key=lambda k: per[k])
+    bound, ach, peak, unit = kern[dom]
+    traffic = None
+    if os.path.exists(args.traffic):
+        try:
+            with open(args.traffic) as f:
+                for line in f:
+                    if line.startswith("hbm_bytes_per_launch"):
+                        traffic = float(line.split("=", 1)[1])
+        except (OSError, ValueError):
+            traffic = None
+    res = {
+        "metric": METRIC,
+        "value": round(mla_tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 (MLA) / fp8-e4m3 (indexer) / fp32 (top-k keys)",
+        "data": "synthetic (seeded N(0,1) inputs, random-init; no checkpoints)",
+        "config": {"workload": "dsa_layer_128k (BASELINE config 5)", "prefill_chunk_tokens": S1,
+                   "context_tokens": S2, "heads": H, "d_qk": DQK, "d_v": DV, "topk": TOPK,
+                   "index_heads": IDX_HEADS, "index_dim": IDX_DIM, "decode_batch": args.dec_batch,
+                   "page_size": 64},
+        "mla_frac_of_bf16_peak": round(mla_tflops / PEAK_BF16_TFLOPS, 4),
+        "indexer_us": round(per["indexer"], 2),
+        "topk_us": round(per["topk"], 2),
+        "indexer_topk_us": round(per["indexer"] + per["topk"], 2),
+        "indexer_tflops": round(idx_tflops, 2),
+        "indexer_frac_of_fp8_peak": round(idx_tflops / PEAK_FP8_TFLOPS, 4),
+        "topk_gbs": round(topk_gbs, 1),
+        "mla_us": round(per["mla"], 2),
+        "decode_us": {"indexer": round(per["dec_indexer"], 2), "topk": round(per["dec_topk"], 2),
+                      "mla": round(per["dec_mla"], 2)},
+        "roofline": {"kernel": dom, "bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
+                     "frac": round(ach / peak, 4), "traffic": traffic},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(S1, S2)
+    print(json.dumps(res))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
