@@ -11,28 +11,41 @@
 // valid index yields out = 0, lse = -inf.  An optional per-head sink adds
 // exp(sink - m) to the denominator (sparse_flash_mla_golden.py:115-149).
 //
-// Work decomposition.  One workgroup (8 waves) handles one token, up to 128
-// heads (one 16-head group per wave; waves past H only help with the gather)
-// and one slice ("split") of the token's index list.
-// Each step gathers 32 indexed KV rows (one 1152-byte row per key) into LDS:
-// row-major for the score product and transposed (V^T) for the PV product, the
-// transpose being done while writing LDS.  Per wave and step:
+// Work decomposition.  One workgroup (8 waves, two per SIMD) handles one token,
+// up to 128 heads (one 16-head MFMA tile per wave; waves past H only help with
+// the gather) and one slice ("split") of the token's index list.  The indexed
+// KV rows (1152 bytes each) are gathered 32 at a time straight into a 4-stage
+// LDS ring with global_load_lds (three steps in flight while one is computed,
+// no staging registers).  A stage is 36 blocks of 1 KB; block (key group kg,
+// chunk group cg) at (cg * 4 + kg) * 1024 holds keys 8kg .. 8kg+7 x 16-byte chunks
+// 8cg .. 8cg+7, key-major, with chunk c of key k (in-block indices) stored at
+// slot k * 8 + (c ^ k ^ (kg & 1)).  One global_load_lds then fetches whole
+// 128-byte lines (8 chunks of one key per 8 lanes), and the XOR swizzle keeps
+// both LDS read patterns below free of bank conflicts.  Per wave and step:
 //   S^T[32 keys x 16 heads] = K[32 x Dqk] . Q^T        (v_mfma_f32_16x16x32_bf16)
-//   O^T[512 x 16 heads]    += V^T[512 x 32] . P^T     (same instruction)
-// Computing S^T rather than S leaves each lane holding exactly the 8
-// probabilities (one head, 8 keys) that the PV instruction wants as its B
-// operand, so P never leaves registers.  The online softmax runs in the exp2
-// domain in registers.  The next step's rows are fetched into registers while
-// the current step computes.  With more than one split the workgroups write
-// normalised partial outputs plus their LSE, and a combine kernel merges them.
+//   O^T[512 x 16 heads]    += V^T[512 x 32] . P^T
+// Computing S^T leaves each lane holding exactly the 8 probabilities (one head,
+// 8 keys) that the PV instruction takes as its B operand, so P never leaves
+// registers.  The V^T operand is read from the same tile with the transposing
+// LDS load ds_read_b64_tr_b16, so V is never copied.  The softmax keeps a
+// reference maximum per head and rescales O only when a score exceeds it by
+// more than 2^8.  With more than one split the workgroups write normalised
+// partial outputs plus their LSE, and a combine kernel merges them.
 #include "dsa_common.h"
 
 namespace {
 
 constexpr int kKT = 32;          // keys per step
 constexpr int kDV = 512;         // value dim
-constexpr int kVtStride = 80;    // bytes per V^T row in LDS (32 keys * 2 + 16 pad)
+constexpr int kWaves = 8;
+constexpr int kHeadsPerGroup = 16 * kWaves;
+constexpr int kStages = 4;
 constexpr int kMaxKeysPerSplit = 2048;
+constexpr float kSlack = 8.f;    // log2 headroom of the reference maximum
+
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short i16x8;
+#define DSA_LDS __attribute__((address_space(3)))
 
 struct MlaParams {
   const uint16_t* q;            // [T, H, Dqk]
@@ -55,30 +68,94 @@ struct MlaParams {
   int causal;
 };
 
-// Slot of key k (0..31) in a V^T row: slot 8g + j holds key 16*(j/4) + 4g + j%4,
-// the order in which lane group g holds its 8 probabilities.
-__device__ __forceinline__ int vt_slot(int k) {
-  const int g = (k & 15) >> 2;
-  const int j = 4 * (k >> 4) + (k & 3);
-  return 8 * g + j;
+// s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
-constexpr int kWaves = 8;
-constexpr int kHeadsPerGroup = 16 * kWaves;
+// Transposing LDS read (ds_read_b64_tr_b16) issued as inline asm.  The builtin
+// form makes the compiler drain every in-flight global_load_lds (vmcnt(0))
+// before it, since it cannot tell the two apart; here the caller orders the
+// read after the step's barrier and waits for its result with lds_wait<N>.
+template <int OFF>
+__device__ __forceinline__ dsa::i32x2 lds_read_tr16(uint32_t addr) {
+  dsa::i32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+// 16-byte LDS read issued as inline asm, for the same reason: it pins how far
+// ahead of their MFMAs the reads run.
+template <int OFF>
+__device__ __forceinline__ dsa::i32x4 lds_read_b128(uint32_t addr) {
+  dsa::i32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void lds_wait1(dsa::i32x4& a) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "i"(N));
+}
+// s_waitcnt lgkmcnt(N); the registers passed in are tied to the wait so that no
+// use of them is scheduled before it.
+template <int N>
+__device__ __forceinline__ void lds_wait(dsa::i32x2& a, dsa::i32x2& b) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+// Compile-time loop: f(IntC<B>{}), ..., f(IntC<E - 1>{}).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(IntC<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// Cross-lane reductions over the lane groups l ^ 16 and l ^ 32 (gfx950 permlane swaps).
+__device__ __forceinline__ float xor16_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Source of the gathers for invalid keys: always in bounds, always zero.
+__device__ __align__(16) uint16_t g_zero_row[576];
 
 template <int DQK>
 __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
   constexpr int NT = kWaves * 64;
   constexpr int KSTEPS = DQK / 32;          // MFMA k-steps of the score product
   constexpr int NCH = DQK / 8;              // 16-byte chunks per KV row
-  constexpr int KROW = DQK * 2 + 16;        // padded LDS row (bytes)
-  constexpr int NTASK = 16 * NCH;           // (key pair, chunk) copy tasks per step
-  constexpr int NITER = (NTASK + NT - 1) / NT;
+  constexpr int STAGE = kKT * DQK * 2;      // bytes per ring stage
+  // wave w's i-th load fills block (kg = w % 4, cg = 2i + w / 4): waves 0-3 own
+  // the even chunk groups, waves 4-7 the odd ones
+  static_assert(NCH % 8 == 0, "whole chunk groups");
+  constexpr int NCG = NCH / 8;                    // chunk groups: 9 (576) or 8 (512)
+  constexpr int LOADS_HI = (NCG + 1) / 2;         // loads per step of waves 0-3
+  constexpr int LOADS_LO = NCG / 2;               // loads per step of waves 4-7
+  static_assert(2 * LOADS_HI < 64, "vmcnt range");
 
   extern __shared__ __align__(16) unsigned char smem[];
-  unsigned char* ktile = smem;                                   // [32][KROW]
-  unsigned char* vt = smem + kKT * KROW;                         // [512][kVtStride]
-  int64_t* rows = reinterpret_cast<int64_t*>(vt + kDV * kVtStride);  // [keys_per_split]
+  int32_t* rows = reinterpret_cast<int32_t*>(smem + kStages * STAGE);  // [keys_per_split]
 
   // ---- workgroup -> (token, head group, split); head groups of one (token,
   // split) share an XCD so the second gather of the same rows hits L2.
@@ -101,6 +178,17 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
   const int kbeg = split * p.keys_per_split;
   const int nkeys = max(0, min(p.keys_per_split, p.topk - kbeg));
 
+  // ---- Q^T operand: lane (g, c) holds head c, dims 32ks + 8g .. +8
+  dsa::bf16x8 qf[KSTEPS];
+  {
+    const uint16_t* qp = p.q + (token * p.H + (head_ok ? head : 0)) * DQK + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      dsa::i32x4 v = head_ok ? *reinterpret_cast<const dsa::i32x4*>(qp + 32 * ks) : dsa::i32x4{0, 0, 0, 0};
+      qf[ks] = __builtin_bit_cast(dsa::bf16x8, v);
+    }
+  }
+
   // ---- resolve this split's indices to physical rows (-1 = skip) ----
   {
     const int kvl = p.kv_len ? p.kv_len[b] : (int)(p.skv < 0x7fffffff ? p.skv : 0x7fffffff);
@@ -108,7 +196,7 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
     const int32_t* ip = p.indices + token * p.topk + kbeg;
     for (int j = tid; j < nkeys; j += NT) {
       const int idx = ip[j];
-      int64_t row = -1;
+      int32_t row = -1;
       bool ok = idx >= 0 && idx < kvl && (int64_t)idx < p.skv;
       if (ok && p.causal) ok = idx <= qs + s;
       if (ok) {
@@ -116,76 +204,42 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
           const int blk = idx / p.block_size;
           const int page = blk < p.max_blocks ? p.block_table[(int64_t)b * p.max_blocks + blk] : -1;
           const int64_t rr = (int64_t)page * p.block_size + idx % p.block_size;
-          if (page >= 0 && rr < p.pool_rows) row = rr;
+          if (page >= 0 && rr < p.pool_rows) row = (int32_t)rr;
         } else {
-          row = (int64_t)b * p.skv + idx;
+          row = (int32_t)((int64_t)b * p.skv + idx);
         }
       }
       rows[j] = row;
     }
   }
-
-  // ---- Q^T operand for this wave's 16 heads: lane (g, c) = head c, dims 32ks + 8g .. +8
-  dsa::bf16x8 qf[KSTEPS];
-  {
-    const uint16_t* qp = p.q + (token * p.H + (head_ok ? head : 0)) * DQK + 8 * g;
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-      dsa::i32x4 v = head_ok ? *reinterpret_cast<const dsa::i32x4*>(qp + 32 * ks)
-                             : dsa::i32x4{0, 0, 0, 0};
-      qf[ks] = __builtin_bit_cast(dsa::bf16x8, v);
-    }
-  }
+  wait_vmcnt<0>();  // Q operands are in registers before any gather is queued
   __syncthreads();  // rows[] ready
 
-  // ---- gather helpers: task q -> key pair m = q % 16, chunk ch = q / 16
-  dsa::i32x4 pf[NITER][2];
-  auto fetch = [&](int step) {
+  // ---- gather of step `step` into ring stage step % kStages.  Wave w fills the
+  // blocks (kg = w % 4, cg = 2i + w / 4), i = 0, 1, ...; lane l loads in-block
+  // key l / 8 and chunk (l % 8) ^ (l / 8) ^ (kg & 1), so it lands in slot l.
+  const int gkg = wave & 3;
+  const int gkey = 8 * gkg + (lane >> 3);
+  const int gch0 = 8 * (wave >> 2) + ((lane & 7) ^ (lane >> 3) ^ (gkg & 1));
+  const bool many = (wave >> 2) == 0;  // waves 0-3 issue LOADS_HI loads per step
+  auto issue = [&](int step) {
+    unsigned char* sb = smem + (step % kStages) * STAGE;
+    const int kk = step * kKT + gkey;
+    const int32_t rr = kk < nkeys ? rows[kk] : -1;
+    const uint16_t* src = (rr >= 0 ? p.kv + (int64_t)rr * DQK : g_zero_row) + 8 * gch0;
 #pragma unroll
-    for (int it = 0; it < NITER; ++it) {
-      const int t = tid + it * NT;
-      const int m = t & 15, ch = t >> 4;
-      const int kk = step * kKT + 2 * m;
-      dsa::i32x4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
-      if (t < NTASK) {
-        const int64_t r0 = kk < nkeys ? rows[kk] : -1;
-        const int64_t r1 = kk + 1 < nkeys ? rows[kk + 1] : -1;
-        if (r0 >= 0) v0 = *reinterpret_cast<const dsa::i32x4*>(p.kv + r0 * DQK + 8 * ch);
-        if (r1 >= 0) v1 = *reinterpret_cast<const dsa::i32x4*>(p.kv + r1 * DQK + 8 * ch);
-      }
-      pf[it][0] = v0;
-      pf[it][1] = v1;
-    }
-  };
-  auto stash = [&]() {
-#pragma unroll
-    for (int it = 0; it < NITER; ++it) {
-      const int t = tid + it * NT;
-      if (t < NTASK) {
-        const int m = t & 15, ch = t >> 4;
-        const int k0 = 2 * m;
-        *reinterpret_cast<dsa::i32x4*>(ktile + k0 * KROW + 16 * ch) = pf[it][0];
-        *reinterpret_cast<dsa::i32x4*>(ktile + (k0 + 1) * KROW + 16 * ch) = pf[it][1];
-        if (ch < kDV / 8) {
-          const int slot = vt_slot(k0);  // k0 + 1 sits in slot + 1
-          unsigned char* dst = vt + (8 * ch) * kVtStride + 2 * slot;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t a = (uint32_t)pf[it][0][e], bb = (uint32_t)pf[it][1][e];
-            // element 2e (low halves) and 2e + 1 (high halves) of both keys
-            *reinterpret_cast<uint32_t*>(dst + (2 * e) * kVtStride) = (a & 0xffffu) | (bb << 16);
-            *reinterpret_cast<uint32_t*>(dst + (2 * e + 1) * kVtStride) = (a >> 16) | (bb & 0xffff0000u);
-          }
-        }
-      }
+    for (int i = 0; i < LOADS_HI; ++i) {
+      if (i < LOADS_LO || many)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + 8 * 16 * i),
+                                         (DSA_LDS void*)(sb + (i * kWaves + wave) * 1024), 16, 0, 0);
     }
   };
 
-  // ---- online-softmax state: lane (g, c) owns head c
-  float m_run = -__builtin_inff();
+  // ---- softmax state: lane (g, c) owns head c
+  float m_ref = -__builtin_inff();
   float l_run = 0.f;
   if (p.sink != nullptr && split == 0 && head_ok) {
-    m_run = p.sink[head] * dsa::kLog2e;
+    m_ref = p.sink[head] * dsa::kLog2e;
     l_run = g == 0 ? 1.f : 0.f;
   }
   dsa::f32x4 o[kDV / 16];
@@ -193,102 +247,161 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
   for (int dt = 0; dt < kDV / 16; ++dt) o[dt] = dsa::f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int nsteps = (nkeys + kKT - 1) / kKT;
-  if (nsteps > 0) {
-    fetch(0);
-    stash();
-  }
-  __syncthreads();
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st)
+    if (st < nsteps) issue(st);
 
   for (int step = 0; step < nsteps; ++step) {
-    const bool more = step + 1 < nsteps;
-    if (more) fetch(step + 1);
+    // this wave's gathers for `step` are done once at most the younger ones
+    // (up to kStages - 2 steps) are outstanding; the barrier publishes all waves'
+    const int younger = min(kStages - 2, nsteps - 1 - step);
+    if (many) {
+      if (younger >= 2) wait_vmcnt<2 * LOADS_HI>();
+      else if (younger == 1) wait_vmcnt<LOADS_HI>();
+      else wait_vmcnt<0>();
+    } else {
+      if (younger >= 2) wait_vmcnt<2 * LOADS_LO>();
+      else if (younger == 1) wait_vmcnt<LOADS_LO>();
+      else wait_vmcnt<0>();
+    }
+    __builtin_amdgcn_s_barrier();
+    // the stage read in the previous step is free for step + kStages - 1
+    if (step + kStages - 1 < nsteps) issue(step + kStages - 1);
 
     if (wave_active) {
-    // S^T = K . Q^T : acc[kt][i] = score(key 16kt + 4g + i, head c)
-    dsa::f32x4 acc[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      acc[kt] = dsa::f32x4{0.f, 0.f, 0.f, 0.f};
-      const unsigned char* kp = ktile + (16 * kt + c) * KROW + 16 * g;
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        const dsa::bf16x8 a = __builtin_bit_cast(dsa::bf16x8, *reinterpret_cast<const dsa::i32x4*>(kp + 64 * ks));
-        acc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], acc[kt], 0, 0, 0);
-      }
-    }
+      const unsigned char* sb = smem + (step % kStages) * STAGE;
+      // S^T = K . Q^T : acc[kt][i] = score(key 16kt + 4g + i, head c); the A
+      // fragment of (kt, ks) is chunk 4ks + g of key 16kt + c.  Reads run
+      // kPre fragments ahead of the MFMAs that consume them.
+      dsa::f32x4 acc[2] = {dsa::f32x4{0.f, 0.f, 0.f, 0.f}, dsa::f32x4{0.f, 0.f, 0.f, 0.f}};
+      // A fragment (kt, ks) = chunk 4ks + g of key 16kt + c: block (kg = 2kt + c/8,
+      // cg = ks/2), in-block key c%8, in-block chunk 4(ks%2) + g  ->  byte offset
+      //   (ks/2) 4096 + kt 2048 + (ks%2 ? kq1 : kq0)
+      const int qkin = c & 7, qkg1 = (c >> 3) & 1;
+      const int qm = qkin ^ qkg1;  // swizzle of this lane's key
+      const uint32_t qbase = (uint32_t)(size_t)(DSA_LDS unsigned char*)(sb + qkg1 * 1024 + qkin * 128 + 16 * (g ^ (qm & 3)));
+      const uint32_t kq0 = qbase + 64 * (qm >> 2);
+      const uint32_t kq1 = qbase + 64 * (1 ^ (qm >> 2));
+      // fragment f = 2 ks + kt; kPre fragments in flight
+      constexpr int kPre = 4;
+      dsa::i32x4 kfr[kPre];
+      // fragment f: ks = f / 2, kt = f % 2
+      static_for<0, kPre>([&](auto F) {
+        constexpr int f = decltype(F)::value;
+        kfr[f] = lds_read_b128<(f >> 2) * 4096 + (f & 1) * 2048>((f >> 1) & 1 ? kq1 : kq0);
+      });
+      static_for<0, 2 * KSTEPS>([&](auto F) {
+        constexpr int f = decltype(F)::value;
+        constexpr int younger = (2 * KSTEPS - 1 - f) < (kPre - 1) ? (2 * KSTEPS - 1 - f) : (kPre - 1);
+        lds_wait1<younger>(kfr[f % kPre]);
+        const dsa::i32x4 cur = kfr[f % kPre];
+        constexpr int fn = f + kPre;
+        if constexpr (fn < 2 * KSTEPS)
+          kfr[f % kPre] = lds_read_b128<(fn >> 2) * 4096 + (fn & 1) * 2048>((fn >> 1) & 1 ? kq1 : kq0);
+        acc[f & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dsa::bf16x8, cur), qf[f >> 1],
+                                                             acc[f & 1], 0, 0, 0);
+      });
 
-    // mask + scale (log2 domain) and the tile max per head
-    float sv[2][4];
-    float tmax = -__builtin_inff();
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kk = step * kKT + 16 * kt + 4 * g + i;
-        const bool ok = kk < nkeys && rows[kk] >= 0;
-        sv[kt][i] = ok ? acc[kt][i] * p.scale_log2 : -__builtin_inff();
-        tmax = fmaxf(tmax, sv[kt][i]);
-      }
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    float alpha = 1.f;
-    float pr[2][4];
-    if (m_new == -__builtin_inff()) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pr[kt][i] = 0.f;
-    } else {
-      alpha = exp2f(m_run - m_new);
-      float psum = 0.f;
+      // validity of the step's 32 keys as a wave-uniform bit mask
+      const int mk = step * kKT + (lane & 31);
+      const uint32_t vmask = (uint32_t)__ballot(mk < nkeys && rows[mk] >= 0);
+      float sv[2][4];
+      float tmax = -__builtin_inff();
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          pr[kt][i] = exp2f(sv[kt][i] - m_new);
-          psum += pr[kt][i];
+          sv[kt][i] = acc[kt][i];
+          tmax = fmaxf(tmax, sv[kt][i]);
         }
-      l_run = l_run * alpha + psum;
-    }
-    m_run = m_new;
-    if (!__all(alpha == 1.f)) {
+      if (vmask != 0xffffffffu) {
+        tmax = -__builtin_inff();
 #pragma unroll
-      for (int dt = 0; dt < kDV / 16; ++dt)
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[dt][i] *= alpha;
-    }
-
-    // P^T operand: slots 0..3 = keys 4g..4g+3, slots 4..7 = keys 16+4g..16+4g+3
-    dsa::i32x4 pb;
-    pb[0] = (int)dsa::pack_bf16x2(pr[0][0], pr[0][1]);
-    pb[1] = (int)dsa::pack_bf16x2(pr[0][2], pr[0][3]);
-    pb[2] = (int)dsa::pack_bf16x2(pr[1][0], pr[1][1]);
-    pb[3] = (int)dsa::pack_bf16x2(pr[1][2], pr[1][3]);
-    const dsa::bf16x8 pbf = __builtin_bit_cast(dsa::bf16x8, pb);
-
-    // O^T[d, head] += V^T[d, slots] . P^T[slots, head]
-    const unsigned char* vp = vt + c * kVtStride + 16 * g;
+          for (int i = 0; i < 4; ++i) {
+            if (!((vmask >> (16 * kt + 4 * g + i)) & 1u)) sv[kt][i] = -__builtin_inff();
+            tmax = fmaxf(tmax, sv[kt][i]);
+          }
+      }
+      // scores stay raw (unscaled) until the exponent: s * scale_log2 - m_ref
+      tmax = xor32_max(xor16_max(tmax)) * p.scale_log2;
+      // m_ref is a reference maximum, not the running one: probabilities are
+      // exp2(s - m_ref) and may reach 2^kSlack before O and l move to a new
+      // reference.  Exact in fp32 / bf16 (relative precision is unchanged) and
+      // it turns the per-step rescale of O into a rare event.
+      if (__any(tmax > m_ref + kSlack)) {
+        const float m_new = fmaxf(m_ref, tmax);
+        const float alpha = m_new == -__builtin_inff() ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+        l_run *= alpha;
 #pragma unroll
-    for (int dt = 0; dt < kDV / 16; ++dt) {
-      const dsa::bf16x8 a = __builtin_bit_cast(dsa::bf16x8, *reinterpret_cast<const dsa::i32x4*>(vp + dt * 16 * kVtStride));
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pbf, o[dt], 0, 0, 0);
-    }
-    }  // wave_active
+        for (int dt = 0; dt < kDV / 16; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[dt][i] *= alpha;
+        m_ref = m_new;
+      }
+      const float mref = m_ref == -__builtin_inff() ? 0.f : m_ref;
+      float pr[2][4];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pr[kt][i] = __builtin_amdgcn_exp2f(fmaf(sv[kt][i], p.scale_log2, -mref));
+          l_run += pr[kt][i];
+        }
+      // P^T operand: element 4kt + i = key 16kt + 4g + i
+      dsa::i32x4 pb;
+      pb[0] = (int)dsa::pack_bf16x2(pr[0][0], pr[0][1]);
+      pb[1] = (int)dsa::pack_bf16x2(pr[0][2], pr[0][3]);
+      pb[2] = (int)dsa::pack_bf16x2(pr[1][0], pr[1][1]);
+      pb[3] = (int)dsa::pack_bf16x2(pr[1][2], pr[1][3]);
+      const dsa::bf16x8 pbf = __builtin_bit_cast(dsa::bf16x8, pb);
 
-    __syncthreads();
-    if (more) stash();
-    __syncthreads();
+      // O^T[d, head] += V^T[d, keys] . P^T[keys, head].  The transposing load:
+      // lane s of group g points at V[16r + 4g + s/4][16dt + 4(s%4)] (chunk
+      // 2dt + (s%4)/2, byte 8 (s%2)) and lane o receives V[16r + 4g + j][16dt + o]
+      // for j = 0..3 (elements 4r + j).
+      // transposing read r of d-tile dt, lane (g, s = c): key 16r + 4g + s/4 -> block
+      // kg = 2r + g/2, in-block key k = 4(g%2) + s/4; chunk 2dt + h (h = (s%4)/2) ->
+      // cg = dt/4, in-block chunk 2(dt%4) + h; byte 8(s%2).  With m = k ^ (kg & 1):
+      //   offset = (dt/4) 4096 + r 2048 + vq[dt % 4],  vq[e] = vbase + 32 (e ^ (m / 2))
+      const int sub = c & 3;
+      const int vk = 4 * (g & 1) + (c >> 2);
+      const int vm = vk ^ ((g >> 1) & 1);
+      const uint32_t vbase = (uint32_t)(size_t)(DSA_LDS unsigned char*)(sb + (g >> 1) * 1024 + vk * 128 + 16 * ((sub >> 1) ^ (vm & 1)) + 8 * (sub & 1));
+      uint32_t vq[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vq[e] = vbase + 32 * (e ^ (vm >> 1));
+      // kVPre fragment pairs in flight; pair dt is complete once at most the
+      // younger pairs (2 reads each) are outstanding
+      constexpr int kVPre = 4;
+      dsa::i32x2 vfr[kVPre][2];
+      static_for<0, kVPre>([&](auto F) {
+        constexpr int f = decltype(F)::value;
+        vfr[f][0] = lds_read_tr16<(f >> 2) * 4096>(vq[f & 3]);
+        vfr[f][1] = lds_read_tr16<(f >> 2) * 4096 + 2048>(vq[f & 3]);
+      });
+      static_for<0, kDV / 16>([&](auto D) {
+        constexpr int dt = decltype(D)::value;
+        constexpr int younger = (kDV / 16 - 1 - dt) < (kVPre - 1) ? (kDV / 16 - 1 - dt) : (kVPre - 1);
+        lds_wait<2 * younger>(vfr[dt % kVPre][0], vfr[dt % kVPre][1]);
+        const dsa::i32x2 v0 = vfr[dt % kVPre][0], v1 = vfr[dt % kVPre][1];
+        constexpr int dn = dt + kVPre;
+        if constexpr (dn < kDV / 16) {
+          vfr[dt % kVPre][0] = lds_read_tr16<(dn >> 2) * 4096>(vq[dn & 3]);
+          vfr[dt % kVPre][1] = lds_read_tr16<(dn >> 2) * 4096 + 2048>(vq[dn & 3]);
+        }
+        const dsa::i32x4 av = {v0[0], v0[1], v1[0], v1[1]};
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dsa::bf16x8, av), pbf, o[dt], 0, 0, 0);
+      });
+    }
   }
 
   // ---- epilogue: lane (g, c) holds O^T[16dt + 4g + i][head c]
-  float l_tot = l_run;
-  l_tot += __shfl_xor(l_tot, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
+  const float l_tot = xor32_sum(xor16_sum(l_run));
   const bool has = l_tot > 0.f;
   const float inv = has ? 1.f / l_tot : 0.f;
-  const float lse_v = has ? (m_run + log2f(l_tot)) * dsa::kLn2 : -__builtin_inff();
+  const float lse_v = has ? (m_ref + __builtin_amdgcn_logf(l_tot)) * dsa::kLn2 : -__builtin_inff();
   if (!head_ok) return;
   if (p.nsplit == 1) {
     uint16_t* op = p.out + (token * p.H + head) * kDV + 4 * g;
@@ -348,8 +461,7 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
 
 template <int DQK>
 int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
-  constexpr int KROW = DQK * 2 + 16;
-  const size_t smem = (size_t)kKT * KROW + (size_t)kDV * kVtStride + sizeof(int64_t) * (size_t)p.keys_per_split;
+  const size_t smem = (size_t)kStages * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split;
   auto fn = sparse_mla_kernel<DQK>;
   hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess)
@@ -360,9 +472,10 @@ int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
 }
 
 int choose_splits(int64_t tokens, int nhg, int topk) {
-  // enough workgroups to cover the 256 CUs about twice; keep >= 256 keys per split
+  // one workgroup per CU fits (LDS); split the index list until the 256 CUs are
+  // covered, keeping >= 256 keys per split
   int ns = 1;
-  while (tokens * nhg * ns < 512 && (topk + 2 * ns - 1) / (2 * ns) >= 256) ns *= 2;
+  while (tokens * nhg * ns < 256 && (topk + 2 * ns - 1) / (2 * ns) >= 256) ns *= 2;
   while ((topk + ns - 1) / ns > kMaxKeysPerSplit) ++ns;
   return ns;
 }
@@ -393,12 +506,16 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
     return set_error(kUnsupported, "dsa_sparse_mla_fwd: d_qk must be 576 or 512 (got %d)", d_qk);
   if (B < 0 || S < 0 || H <= 0 || topk < 0 || skv < 0)
     return set_error(kInvalidArgument, "dsa_sparse_mla_fwd: bad sizes");
+  if (!(sm_scale > 0.f) || sm_scale == __builtin_inff())
+    return set_error(kInvalidArgument, "dsa_sparse_mla_fwd: sm_scale must be positive and finite");
   if (block_table != nullptr && (block_size <= 0 || max_blocks <= 0))
     return set_error(kInvalidArgument, "dsa_sparse_mla_fwd: paged KV needs block_size > 0 and max_blocks > 0");
   const int64_t T = B * S;
   if (T == 0) return kOk;
   if (q == nullptr || kv == nullptr || indices == nullptr || out == nullptr)
     return set_error(kInvalidArgument, "dsa_sparse_mla_fwd: null pointer");
+  if ((block_table ? skv : B * skv) >= ((int64_t)1 << 31))
+    return set_error(kUnsupported, "dsa_sparse_mla_fwd: more than 2^31 - 1 KV rows");
 
   MlaParams p;
   p.q = static_cast<const uint16_t*>(q);
