@@ -1,4 +1,4 @@
-// Row-wise top-k over fp32 scores for gfx950: exact radix select + LDS sort.
+// Row-wise top-k over fp32 scores for gfx950: exact radix select + register sort.
 //
 // Contract (the lightning indexer golden, examples/deepseek_v4/lightning_indexer.py:316-325):
 //   out[r, :] = argsort(-x[r, :L_r], stable=True)[:K]  (descending value, ties to
@@ -10,12 +10,20 @@
 // where ordered() maps fp32 onto uint32 monotonically (-0.0 folded onto +0.0 so
 // they tie, NaN placed below -inf as torch.sort places it last).  All C are
 // distinct and "C larger" == "earlier in the stable descending order", so the
-// top-K set is exactly {C >= C_K} for the K-th largest composite C_K.  C_K is
-// found digit by digit (12-bit digits) with LDS histograms; each pass narrows
-// the group that holds C_K.  Once the group is small it is copied to LDS and the
-// remaining digits are resolved there, so a row is read from HBM once (rows up
-// to 32K are held in registers) or twice (longer rows, streamed).  The K chosen
-// composites are then bitonic-sorted in LDS (descending) and written out.
+// top-K set is exactly {C >= C_K} for the K-th largest composite C_K.
+//
+// Selection.  C_K is found digit by digit (12-bit digits, LDS histograms).
+//  * Rows of up to 32K elements are held in registers and read from HBM once.
+//  * Longer rows: a sample of the row (64-element blocks spread over it) gives a
+//    threshold T whose estimated count above it is ~1.25 K; one vectorised pass
+//    then copies every element >= T into LDS.  If at least K and at most the LDS
+//    capacity landed there, the top K are exactly among them and the remaining
+//    digits are resolved in LDS; otherwise exact histogram passes over the row
+//    take over.
+// Ordering.  The K chosen composites are bitonic-sorted (descending) by 256
+// threads holding 8 (or 32) keys each: strides below 8 stay in registers,
+// strides up to 256 use cross-lane shuffles, only the largest strides go
+// through LDS (3 barriers for K = 2048).
 #include "dsa_common.h"
 
 namespace {
@@ -24,7 +32,9 @@ constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kHistBits = 12;
 constexpr int kBins = 1 << kHistBits;
-constexpr int kCandCap = 4096;
+constexpr int kCandCap = 5888;     // LDS candidate capacity (46 KB; two blocks fit per CU)
+constexpr int kSortThreads = 256;
+constexpr int kSampleBlocks = 128; // 64-element blocks sampled from a long row
 
 __device__ __forceinline__ uint32_t ordered_key(float f) {
   uint32_t u = __float_as_uint(f);
@@ -41,6 +51,9 @@ __device__ __forceinline__ float key_value(uint32_t k) {
 __device__ __forceinline__ uint64_t composite(uint32_t key, uint32_t idx) {
   return ((uint64_t)key << 32) | (uint64_t)(~idx);
 }
+
+// C >> s for s in [0, 64] (a shift by 64 is not defined on uint64_t).
+__device__ __forceinline__ uint64_t high_bits(uint64_t C, int s) { return s >= 64 ? 0ull : C >> s; }
 
 struct Shared {
   uint32_t hist[kBins];
@@ -64,7 +77,8 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
   if (lane == 63) wsum[wid] = x;
   __syncthreads();
   uint32_t pre = 0;
-  for (int w = 0; w < wid; ++w) pre += wsum[w];
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) pre += w < wid ? wsum[w] : 0u;  // independent loads
   __syncthreads();
   return pre + x - v;
 }
@@ -79,18 +93,21 @@ __device__ __forceinline__ void find_bucket(Shared& sh, uint32_t need) {
   uint32_t local = h0 + h1 + h2 + h3;
   uint32_t before = block_exclusive_scan(local, sh.wsum);
   if (before < need && need <= before + local) {
-    uint32_t acc = before;
-    uint32_t hs[4] = {h0, h1, h2, h3};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (acc + hs[i] >= need) {
-        sh.res_bucket = (uint32_t)(top - i);
-        sh.res_above = acc;
-        sh.res_count = hs[i];
-        break;
-      }
-      acc += hs[i];
+    const uint32_t c0 = before + h0, c1 = c0 + h1, c2 = c1 + h2;
+    int i;
+    uint32_t above, count;
+    if (c0 >= need) {
+      i = 0; above = before; count = h0;
+    } else if (c1 >= need) {
+      i = 1; above = c0; count = h1;
+    } else if (c2 >= need) {
+      i = 2; above = c1; count = h2;
+    } else {
+      i = 3; above = c2; count = h3;
     }
+    sh.res_bucket = (uint32_t)(top - i);
+    sh.res_above = above;
+    sh.res_count = count;
   }
   __syncthreads();
 }
@@ -99,53 +116,161 @@ __device__ __forceinline__ void clear_hist(Shared& sh) {
   for (int i = threadIdx.x; i < kBins; i += kThreads) sh.hist[i] = 0u;
 }
 
-// Bitonic sort of buf[0..n) into descending order (n padded to a power of two
-// with zeros, the smallest composite).
-__device__ void sort_desc(uint64_t* buf, int n, int p2) {
-  for (int i = n + threadIdx.x; i < p2; i += kThreads) buf[i] = 0ull;
-  __syncthreads();
-  for (int size = 2; size <= p2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int t = threadIdx.x; t < (p2 >> 1); t += kThreads) {
-        const int i = 2 * t - (t & (stride - 1));
-        const int j = i + stride;
-        const bool desc = (i & size) == 0;
-        uint64_t a = buf[i], b = buf[j];
-        if ((a < b) == desc) {
-          buf[i] = b;
-          buf[j] = a;
-        }
-      }
-      __syncthreads();
-    }
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(IntC<B>{});
+    static_for<B + 1, E>(f);
   }
 }
 
+// x of lane (lane ^ D), D in {1, 2, 4, 8, 16, 32}, with VALU-only cross-lane
+// operations: DPP quad permutes (1, 2), two bank-masked DPP row shifts (4, 8;
+// row_shl:N gives lane i the value of lane i + N, row_shr:N that of lane i - N)
+// and the gfx950 permlane swaps (16, 32).
+template <int D>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t x, int lane) {
+  if constexpr (D == 1) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (D == 2) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (D == 4) {
+    const int t = __builtin_amdgcn_update_dpp((int)x, (int)x, 0x104, 0xF, 0x5, false);  // banks 0,2 <- i+4
+    return (uint32_t)__builtin_amdgcn_update_dpp(t, (int)x, 0x114, 0xF, 0xA, false);   // banks 1,3 <- i-4
+  } else if constexpr (D == 8) {
+    const int t = __builtin_amdgcn_update_dpp((int)x, (int)x, 0x108, 0xF, 0x3, false);  // banks 0,1 <- i+8
+    return (uint32_t)__builtin_amdgcn_update_dpp(t, (int)x, 0x118, 0xF, 0xC, false);   // banks 2,3 <- i-8
+  } else if constexpr (D == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    static_assert(D == 32, "lane distance");
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  }
+}
+
+template <int D>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t x, int lane) {
+  const uint32_t lo = xor_lane<D>((uint32_t)x, lane), hi = xor_lane<D>((uint32_t)(x >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ void cmp_swap(uint64_t& a, uint64_t& b, bool desc) {
+  const uint64_t lo = a < b ? a : b, hi = a < b ? b : a;
+  a = desc ? hi : lo;
+  b = desc ? lo : hi;
+}
+
+// Bitonic sort (descending) of buf[0 .. EPT * 256) by the first 256 threads, each
+// holding EPT consecutive keys; xbuf (same size) is the LDS exchange area for the
+// strides that cross waves.  All threads of the block must call it.
+template <int EPT>
+__device__ void sort_desc(uint64_t* buf, uint64_t* xbuf) {
+  constexpr int N = EPT * kSortThreads;
+  const int t = threadIdx.x;
+  const bool act = t < kSortThreads;
+  uint64_t v[EPT];
+  if (act) {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) v[j] = buf[t * EPT + j];
+  }
+  static_for<1, 16>([&](auto SZ) {
+    constexpr int lsize = decltype(SZ)::value;  // size = 2^lsize
+    if constexpr ((1 << lsize) <= N) {
+      constexpr int size = 1 << lsize;
+      static_for<0, lsize>([&](auto ST) {
+        constexpr int stride = size >> (1 + decltype(ST)::value);
+        if constexpr (stride < EPT) {
+          if (act) {
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) {
+              if ((j & stride) == 0) {
+                const bool desc = ((t * EPT + j) & size) == 0;
+                cmp_swap(v[j], v[j + stride], desc);
+              }
+            }
+          }
+        } else if constexpr (stride < EPT * 64) {
+          if (act) {
+            constexpr int d = stride / EPT;  // partner lane distance within the wave
+            const bool keep_hi = (((t * EPT) & stride) == 0) == (((t * EPT) & size) == 0);
+            const int lane = t & 63;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) {
+              const uint64_t pv = xor_lane64<d>(v[j], lane);
+              const uint64_t hi = v[j] < pv ? pv : v[j], lo = v[j] < pv ? v[j] : pv;
+              v[j] = keep_hi ? hi : lo;
+            }
+          }
+        } else {
+          constexpr int d = stride / EPT;  // partner thread distance (another wave)
+          if (act) {
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) xbuf[t * EPT + j] = v[j];
+          }
+          __syncthreads();
+          if (act) {
+            const bool keep_hi = (((t * EPT) & stride) == 0) == (((t * EPT) & size) == 0);
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) {
+              const uint64_t pv = xbuf[(t ^ d) * EPT + j];
+              const uint64_t hi = v[j] < pv ? pv : v[j], lo = v[j] < pv ? v[j] : pv;
+              v[j] = keep_hi ? hi : lo;
+            }
+          }
+          __syncthreads();
+        }
+      });
+    }
+  });
+  if (act) {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) buf[t * EPT + j] = v[j];
+  }
+  __syncthreads();
+}
+
+struct TopkArgs {
+  const float* x;          // [rows, ld]
+  const int32_t* in_idx;   // [rows, ld] original indices of x's columns, or null (= column)
+  const int32_t* row_len;  // [rows] or null
+  int32_t* out_idx;        // [rows, K]
+  float* out_val;          // [rows, K] or null
+  int64_t ld;
+  int32_t cols, K, pad_invalid, sort;
+};
+
 // ITEMS > 0: the row (length <= ITEMS * 1024) lives in registers, element
-// e = j * 1024 + tid for j < ITEMS.  ITEMS == 0: the row is re-read from global
-// memory on every pass.
-template <int ITEMS>
-__global__ __launch_bounds__(kThreads) void topk_rows_kernel(
-    const float* __restrict__ x, int64_t ld, int32_t cols, const int32_t* __restrict__ row_len,
-    int32_t K, int32_t p2, int32_t pad_invalid, int32_t* __restrict__ out_idx,
-    float* __restrict__ out_val) {
+// e = j * 1024 + tid for j < ITEMS.  ITEMS == 0: the row is streamed.
+// EPT: keys per sorting thread (the sort covers EPT * 256 >= K keys).
+template <int ITEMS, int EPT>
+__global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
+  constexpr int P2 = EPT * kSortThreads;
   extern __shared__ __align__(16) unsigned char smem[];
-  Shared& sh = *reinterpret_cast<Shared*>(smem);
+  Shared* const sh = reinterpret_cast<Shared*>(smem);
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem + ((sizeof(Shared) + 15) & ~size_t(15)));
-  uint64_t* cand = sel + p2;
+  uint64_t* cand = sel + P2;  // max(kCandCap, P2) entries; also the sort's exchange area
 
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
-  const float* xr = x + row * ld;
-  int L = cols;
-  if (row_len != nullptr) {
-    int r = row_len[row];
-    L = r < 0 ? 0 : (r < cols ? r : cols);
+  const float* xr = a.x + row * a.ld;
+  const int32_t* ir = a.in_idx ? a.in_idx + row * a.ld : nullptr;
+  const int K = a.K;
+  int L = a.cols;
+  if (a.row_len != nullptr) {
+    int r = a.row_len[row];
+    L = r < 0 ? 0 : (r < a.cols ? r : a.cols);
   }
   if (tid == 0) {
-    sh.nsel = 0u;
-    sh.ncand = 0u;
+    sh->nsel = 0u;
+    sh->ncand = 0u;
   }
+  auto idx_of = [=](int e) -> uint32_t { return ir ? (uint32_t)ir[e] : (uint32_t)e; };
 
   uint32_t keys[ITEMS > 0 ? ITEMS : 1];
   if constexpr (ITEMS > 0) {
@@ -155,97 +280,151 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(
       keys[j] = e < L ? ordered_key(__builtin_nontemporal_load(xr + e)) : 0u;
     }
   }
+  // visit every element of the row: f(key, element index)
+  auto for_each = [=](auto&& f) {
+    if constexpr (ITEMS > 0) {
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j) {
+        const int e = j * kThreads + tid;
+        if (e < L) f(keys[j], e);
+      }
+    } else {
+      if ((reinterpret_cast<uintptr_t>(xr) & 15) == 0) {
+        constexpr int U = 4;  // float4 loads in flight per thread
+        const int L4 = L & ~3;
+        for (int base = 4 * tid; base < L4; base += 4 * kThreads * U) {
+          dsa::f32x4 v[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int e = base + 4 * kThreads * u;
+            v[u] = e < L4 ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e))
+                          : dsa::f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int e = base + 4 * kThreads * u;
+            if (e < L4) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) f(ordered_key(v[u][q]), e + q);
+            }
+          }
+        }
+        for (int e = L4 + tid; e < L; e += kThreads) f(ordered_key(xr[e]), e);
+      } else {
+        for (int e = tid; e < L; e += kThreads) f(ordered_key(xr[e]), e);
+      }
+    }
+  };
 
   int nsel_final;
   if (L <= K) {
     // Everything is selected.
     __syncthreads();
-    if constexpr (ITEMS > 0) {
-#pragma unroll
-      for (int j = 0; j < ITEMS; ++j) {
-        const int e = j * kThreads + tid;
-        if (e < L) sel[e] = composite(keys[j], (uint32_t)e);
-      }
-    } else {
-      for (int e = tid; e < L; e += kThreads) sel[e] = composite(ordered_key(xr[e]), (uint32_t)e);
-    }
+    for_each([=](uint32_t key, int e) { sel[e] = composite(key, idx_of(e)); });
     nsel_final = L;
     __syncthreads();
   } else {
-    // ---- pass 1: top 12 bits of the value key ----
-    clear_hist(sh);
-    __syncthreads();
-    if constexpr (ITEMS > 0) {
-#pragma unroll
-      for (int j = 0; j < ITEMS; ++j) {
-        const int e = j * kThreads + tid;
-        if (e < L) atomicAdd(&sh.hist[keys[j] >> 20], 1u);
-      }
-    } else {
-      for (int e = tid; e < L; e += kThreads) atomicAdd(&sh.hist[ordered_key(xr[e]) >> 20], 1u);
-    }
-    __syncthreads();
     uint32_t need = (uint32_t)K;
-    find_bucket(sh, need);
-    uint64_t P = sh.res_bucket;
-    int s = 64 - kHistBits;
-    need -= sh.res_above;
-    uint32_t cnt = sh.res_count;
-    bool done = (cnt == need);
-    __syncthreads();
+    uint64_t P = 0;
+    int s = 64;
+    uint32_t cnt = (uint32_t)L;
+    bool done = false;
+    bool have_cand = false;
 
-    // ---- further passes over the row while the group is too large for LDS ----
-    while (!done && s > 0 && cnt > (uint32_t)kCandCap) {
-      const int w = s < kHistBits ? s : kHistBits;
-      const int s2 = s - w;
-      const uint64_t dmask = (1ull << w) - 1ull;
-      clear_hist(sh);
-      __syncthreads();
-      if constexpr (ITEMS > 0) {
-#pragma unroll
-        for (int j = 0; j < ITEMS; ++j) {
-          const int e = j * kThreads + tid;
-          if (e < L) {
-            const uint64_t C = composite(keys[j], (uint32_t)e);
-            if ((C >> s) == P) atomicAdd(&sh.hist[(uint32_t)((C >> s2) & dmask)], 1u);
+    if constexpr (ITEMS == 0) {
+      // ---- sampled threshold, then one pass collecting everything above it ----
+      uint32_t* samp = reinterpret_cast<uint32_t*>(cand);  // kSampleBlocks * 64 keys
+      constexpr int ns = kSampleBlocks * 64;
+      if (L >= 4 * ns) {
+        for (int i = tid; i < ns; i += kThreads) {
+          const int blk = i >> 6;
+          const int start = (int)(((int64_t)blk * L / kSampleBlocks) & ~63);
+          samp[i] = ordered_key(xr[start + (i & 63)]);
+        }
+        // rank of the threshold inside the sample: ~1.25 K + 64 expected above it
+        const uint32_t r = (uint32_t)(((int64_t)(K + K / 4 + 64) * ns + L - 1) / L);
+        clear_hist(*sh);
+        __syncthreads();
+        for (int i = tid; i < ns; i += kThreads) atomicAdd(&sh->hist[samp[i] >> 20], 1u);
+        __syncthreads();
+        find_bucket(*sh, r);
+        const uint32_t b1 = sh->res_bucket, r2 = r - sh->res_above;
+        __syncthreads();
+        clear_hist(*sh);
+        __syncthreads();
+        for (int i = tid; i < ns; i += kThreads)
+          if ((samp[i] >> 20) == b1) atomicAdd(&sh->hist[(samp[i] >> 8) & 0xfffu], 1u);
+        __syncthreads();
+        find_bucket(*sh, r2);
+        const uint32_t T = (b1 << 20) | (sh->res_bucket << 8);
+        __syncthreads();
+        for_each([=](uint32_t key, int e) {
+          if (key >= T) {
+            const uint32_t slot = atomicAdd(&sh->ncand, 1u);
+            if (slot < (uint32_t)kCandCap) cand[slot] = composite(key, idx_of(e));
           }
+        });
+        __syncthreads();
+        const uint32_t nc = sh->ncand;
+        __syncthreads();
+        if (nc >= (uint32_t)K && nc <= (uint32_t)kCandCap) {
+          // the top K all lie among the candidates: the group is all of them
+          have_cand = true;
+        } else if (tid == 0) {
+          sh->ncand = 0u;  // fall back to the exact passes below
         }
-      } else {
-        for (int e = tid; e < L; e += kThreads) {
-          const uint64_t C = composite(ordered_key(xr[e]), (uint32_t)e);
-          if ((C >> s) == P) atomicAdd(&sh.hist[(uint32_t)((C >> s2) & dmask)], 1u);
-        }
+        __syncthreads();
       }
+    }
+
+    if (!have_cand) {
+      // ---- exact pass 1 over the row: top 12 bits of the value key ----
+      clear_hist(*sh);
       __syncthreads();
-      find_bucket(sh, need);
-      P = (P << w) | sh.res_bucket;
-      s = s2;
-      need -= sh.res_above;
-      cnt = sh.res_count;
+      for_each([=](uint32_t key, int) { atomicAdd(&sh->hist[key >> 20], 1u); });
+      __syncthreads();
+      find_bucket(*sh, need);
+      P = sh->res_bucket;
+      s = 64 - kHistBits;
+      need -= sh->res_above;
+      cnt = sh->res_count;
       done = (cnt == need);
       __syncthreads();
-    }
 
-    // ---- collect: strictly-above elements are selected; the group goes to LDS ----
-    auto collect = [&](uint64_t C) {
-      const uint64_t hi = C >> s;
-      if (hi > P || (done && hi == P)) {
-        sel[atomicAdd(&sh.nsel, 1u)] = C;
-      } else if (hi == P) {
-        cand[atomicAdd(&sh.ncand, 1u)] = C;
+      // ---- further passes over the row while the group is too large for LDS ----
+      while (!done && s > 0 && cnt > (uint32_t)kCandCap) {
+        const int w = s < kHistBits ? s : kHistBits;
+        const int s2 = s - w;
+        const uint64_t dmask = (1ull << w) - 1ull;
+        clear_hist(*sh);
+        __syncthreads();
+        for_each([=](uint32_t key, int e) {
+          const uint64_t C = composite(key, idx_of(e));
+          if (high_bits(C, s) == P) atomicAdd(&sh->hist[(uint32_t)((C >> s2) & dmask)], 1u);
+        });
+        __syncthreads();
+        find_bucket(*sh, need);
+        P = (P << w) | sh->res_bucket;
+        s = s2;
+        need -= sh->res_above;
+        cnt = sh->res_count;
+        done = (cnt == need);
+        __syncthreads();
       }
-    };
-    if constexpr (ITEMS > 0) {
-#pragma unroll
-      for (int j = 0; j < ITEMS; ++j) {
-        const int e = j * kThreads + tid;
-        if (e < L) collect(composite(keys[j], (uint32_t)e));
-      }
-    } else {
-      for (int e = tid; e < L; e += kThreads) collect(composite(ordered_key(xr[e]), (uint32_t)e));
+
+      // ---- collect: strictly-above elements are selected; the group goes to LDS ----
+      for_each([=](uint32_t key, int e) {
+        const uint64_t C = composite(key, idx_of(e));
+        const uint64_t hi = high_bits(C, s);
+        if (hi > P || (done && hi == P)) {
+          sel[atomicAdd(&sh->nsel, 1u)] = C;
+        } else if (hi == P) {
+          cand[atomicAdd(&sh->ncand, 1u)] = C;
+        }
+      });
+      __syncthreads();
     }
-    __syncthreads();
-    const int ncand = (int)sh.ncand;
+    const int ncand = (int)sh->ncand;
 
     // ---- resolve the remaining digits inside the LDS candidate group ----
     // (composites are distinct, so the group shrinks to the single C_K by s == 0)
@@ -253,33 +432,37 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(
       const int w = s < kHistBits ? s : kHistBits;
       const int s2 = s - w;
       const uint64_t dmask = (1ull << w) - 1ull;
-      clear_hist(sh);
+      clear_hist(*sh);
       __syncthreads();
       for (int i = tid; i < ncand; i += kThreads) {
         const uint64_t C = cand[i];
-        if ((C >> s) == P) atomicAdd(&sh.hist[(uint32_t)((C >> s2) & dmask)], 1u);
+        if (high_bits(C, s) == P) atomicAdd(&sh->hist[(uint32_t)((C >> s2) & dmask)], 1u);
       }
       __syncthreads();
-      find_bucket(sh, need);
-      P = (P << w) | sh.res_bucket;
+      find_bucket(*sh, need);
+      P = (P << w) | sh->res_bucket;
       s = s2;
-      need -= sh.res_above;
-      cnt = sh.res_count;
+      need -= sh->res_above;
+      cnt = sh->res_count;
       done = (cnt == need);
       __syncthreads();
     }
     for (int i = tid; i < ncand; i += kThreads) {
       const uint64_t C = cand[i];
-      if ((C >> s) >= P) sel[atomicAdd(&sh.nsel, 1u)] = C;
+      if (high_bits(C, s) >= P) sel[atomicAdd(&sh->nsel, 1u)] = C;
     }
     __syncthreads();
     nsel_final = K;
   }
 
-  sort_desc(sel, nsel_final, p2);
+  if (a.sort) {
+    for (int i = nsel_final + tid; i < P2; i += kThreads) sel[i] = 0ull;  // pad: smallest composite
+    __syncthreads();
+    sort_desc<EPT>(sel, cand);
+  }
 
-  int32_t* orow = out_idx + row * (int64_t)K;
-  float* vrow = out_val ? out_val + row * (int64_t)K : nullptr;
+  int32_t* orow = a.out_idx + row * (int64_t)K;
+  float* vrow = a.out_val ? a.out_val + row * (int64_t)K : nullptr;
   for (int p = tid; p < K; p += kThreads) {
     int32_t idx = -1;
     float val = -__builtin_inff();
@@ -287,58 +470,54 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(
       const uint64_t C = sel[p];
       val = key_value((uint32_t)(C >> 32));
       idx = (int32_t)(~(uint32_t)C);
-      if (pad_invalid && val <= -1e30f) idx = -1;
+      if (a.pad_invalid && val <= -1e30f) idx = -1;
     }
     orow[p] = idx;
     if (vrow) vrow[p] = val;
   }
 }
 
-int next_pow2(int v) {
-  int p = 1;
-  while (p < v) p <<= 1;
-  return p;
+template <int ITEMS, int EPT>
+int launch_rows(const TopkArgs& a, int64_t rows, hipStream_t stream) {
+  constexpr int P2 = EPT * kSortThreads;
+  const size_t smem = ((sizeof(Shared) + 15) & ~size_t(15)) +
+                      sizeof(uint64_t) * (size_t)(P2 + (kCandCap > P2 ? kCandCap : P2));
+  auto fn = topk_rows_kernel<ITEMS, EPT>;
+  (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  hipLaunchKernelGGL(fn, dim3((unsigned)rows), dim3(kThreads), smem, stream, a);
+  return dsa::check_launch("dsa_topk_f32");
+}
+
+template <int EPT>
+int launch_items(const TopkArgs& a, int64_t rows, hipStream_t stream) {
+  const int cols = a.cols;
+  if (cols <= 4 * kThreads) return launch_rows<4, EPT>(a, rows, stream);
+  if (cols <= 8 * kThreads) return launch_rows<8, EPT>(a, rows, stream);
+  if (cols <= 16 * kThreads) return launch_rows<16, EPT>(a, rows, stream);
+  if (cols <= 32 * kThreads) return launch_rows<32, EPT>(a, rows, stream);
+  return launch_rows<0, EPT>(a, rows, stream);
 }
 
 }  // namespace
 
 namespace dsa {
 
-size_t topk_smem_bytes(int K) {
-  const int p2 = next_pow2(K < 1 ? 1 : K);
-  return ((sizeof(Shared) + 15) & ~size_t(15)) + sizeof(uint64_t) * (size_t)(p2 + kCandCap);
-}
-
 int topk_launch(const float* x, int64_t rows, int64_t cols, int64_t ld, const int32_t* row_len,
                 int32_t K, int32_t pad_invalid, int32_t* out_idx, float* out_val,
                 hipStream_t stream) {
   if (rows == 0 || K == 0) return kOk;
-  const int p2 = next_pow2(K);
-  const size_t smem = topk_smem_bytes(K);
-  const dim3 grid((unsigned)rows), block(kThreads);
-  const int c = (int)cols;
-#define DSA_TOPK_LAUNCH(ITEMS)                                                                 \
-  do {                                                                                         \
-    auto fn = topk_rows_kernel<ITEMS>;                                                         \
-    if (smem > 64 * 1024)                                                                      \
-      (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize,   \
-                                (int)smem);                                                    \
-    hipLaunchKernelGGL(fn, grid, block, smem, stream, x, ld, c, row_len, K, p2, pad_invalid,   \
-                       out_idx, out_val);                                                      \
-  } while (0)
-  if (cols <= 4 * kThreads) {
-    DSA_TOPK_LAUNCH(4);
-  } else if (cols <= 8 * kThreads) {
-    DSA_TOPK_LAUNCH(8);
-  } else if (cols <= 16 * kThreads) {
-    DSA_TOPK_LAUNCH(16);
-  } else if (cols <= 32 * kThreads) {
-    DSA_TOPK_LAUNCH(32);
-  } else {
-    DSA_TOPK_LAUNCH(0);
-  }
-#undef DSA_TOPK_LAUNCH
-  return check_launch("dsa_topk_f32");
+  TopkArgs a;
+  a.x = x;
+  a.in_idx = nullptr;
+  a.row_len = row_len;
+  a.out_idx = out_idx;
+  a.out_val = out_val;
+  a.ld = ld;
+  a.cols = (int32_t)cols;
+  a.K = K;
+  a.pad_invalid = pad_invalid;
+  a.sort = 1;
+  return K <= 8 * kSortThreads ? launch_items<8>(a, rows, stream) : launch_items<32>(a, rows, stream);
 }
 
 }  // namespace dsa
@@ -352,8 +531,9 @@ extern "C" int dsa_topk_f32(const float* scores, int64_t rows, int64_t cols, int
                      (long long)rows, (long long)cols, (long long)ld, k);
   if (k > 8192)
     return set_error(kUnsupported, "dsa_topk_f32: k=%d exceeds the supported maximum 8192", k);
-  if (cols >= (int64_t)1 << 31)
-    return set_error(kUnsupported, "dsa_topk_f32: cols=%lld exceeds 2^31-1", (long long)cols);
+  if (cols >= (int64_t)1 << 31 || rows >= (int64_t)1 << 31)
+    return set_error(kUnsupported, "dsa_topk_f32: rows=%lld cols=%lld exceed 2^31-1", (long long)rows,
+                     (long long)cols);
   if (rows > 0 && k > 0 && (scores == nullptr || out_idx == nullptr))
     return set_error(kInvalidArgument, "dsa_topk_f32: null scores or out_idx");
   return topk_launch(scores, rows, cols, ld, row_len, k, pad_invalid, out_idx, out_val,
