@@ -22,8 +22,8 @@
 //    take over.
 // Ordering.  The K chosen composites are bitonic-sorted (descending) by 256
 // threads holding 8 (or 32) keys each: strides below 8 stay in registers,
-// strides up to 256 use cross-lane shuffles, only the largest strides go
-// through LDS (3 barriers for K = 2048).
+// strides up to 256 use VALU cross-lane exchanges (DPP, permlane swaps), only
+// the largest strides go through LDS (3 barriers for K = 2048).
 #include "dsa_common.h"
 
 namespace {

@@ -79,11 +79,11 @@ def topk_selector(x: torch.Tensor, top_k: int, *, row_len: Optional[torch.Tensor
         raise ValueError(f"x must be 2-D [B, N], got shape {tuple(x.shape)}")
     if x.dtype != torch.float32:
         raise ValueError(f"x must be float32, got {x.dtype}")
+    if not (1 <= top_k <= 8192):
+        raise ValueError(f"top_k must be in [1, 8192], got {top_k}")
     dev = _require_gpu(x, row_len)
     _require_contiguous("x", x)
     B, N = x.shape
-    if not (1 <= top_k <= 8192):
-        raise ValueError(f"top_k must be in [1, 8192], got {top_k}")
     rl = _int32_vec("row_len", row_len, B, dev)
     idx = torch.empty((B, top_k), dtype=torch.int32, device=dev)
     val = torch.empty((B, top_k), dtype=torch.float32, device=dev) if return_values else None
