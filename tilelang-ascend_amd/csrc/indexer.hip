@@ -8,26 +8,41 @@
 // see none.  q and k are fp8 e4m3 (OCP, torch.float8_e4m3fn); the per-key fp32
 // scale is applied after the head sum, which is exact because scale > 0.
 //
-// Work decomposition.  One workgroup = 8 waves = 16 query tokens of one batch
-// row x one chunk of keys.  Each wave holds the A operands of its 2 tokens
-// (64 heads x 128 dims each) in registers and streams 64-key tiles of K from a
-// double-buffered LDS ring.  One v_mfma_scale_f32_16x16x128_f8f6f4 computes a
-// 16-head x 16-key block over the whole 128-dim head, so the ReLU, the head
-// weight and the head sum are applied to the accumulator registers directly and
-// only the final fp32 logit is written to HBM.  Workgroups that share a key
-// chunk are placed on the same XCD so the chunk stays in that XCD's L2.
+// Formulation.  ReLU(d) = (d + |d|) / 2, so with u_t = sum_h w[t, h] q[t, h, :]
+//   sum_h w_h ReLU(q_h . k) = ( sum_h w_h |q_h . k|  +  u_t . k ) / 2.
+// The first sum costs one FMA per (head, key) with the |.| source modifier; the
+// second is one more fp8 MFMA per 16 keys whose A rows hold u_t split into four
+// fp8 pieces with power-of-two scales (E8M0 block scales of the MFMA):
+// u = sum_s 2^(e-4s) u_s, exact to 2^-17 of max|u|.  Both terms keep fp32-level
+// accuracy; no rounding of q.k to a narrower type takes place.
+//
+// Work decomposition.  One workgroup = 16 waves = 16 query tokens (one per wave)
+// of one batch row x one chunk of keys.  A wave holds its token's A operands
+// (64 heads x 128 dims of fp8 plus the u pieces) in registers.  K streams through
+// a 4-stage LDS ring of 64-key tiles filled with global_load_lds (three tiles in
+// flight while one is computed); a tile stores 16-byte chunk j of key s at slot
+// j ^ (s & 7) so the B-operand reads are free of bank conflicts.  Per 16-key block
+// a wave issues 5 fp8 MFMAs (v_mfma_scale_f32_16x16x128_f8f6f4) and 17 VALU ops;
+// the 4 lane groups then exchange their partial sums with permlane swaps (a
+// reduce-scatter) so that lane l ends up with key 64-tile + l and the whole tile
+// is one coalesced 256-byte store.  Workgroups that share a key chunk are placed
+// on the same XCD so the chunk stays in that XCD's L2.
 #include "dsa_common.h"
 
 namespace {
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 16;
 constexpr int kThreads = kWaves * 64;
-constexpr int kTokPerWave = 2;
-constexpr int kTokPerBlock = kWaves * kTokPerWave;  // 16
+constexpr int kTokPerBlock = kWaves;  // one query token per wave
 constexpr int kHeads = 64;
 constexpr int kDim = 128;
 constexpr int kKeyTile = 64;
-constexpr int kRowBytes = kDim + 16;  // padded LDS row: conflict-free 16-byte reads
+constexpr int kStages = 4;
+constexpr int kTileBytes = kKeyTile * kDim;      // 8 KB
+constexpr int kKeyLoaders = kTileBytes / 1024;   // waves 0..7 load 1 KB of keys each
+constexpr int kScaleLoader = kKeyLoaders;        // wave 8 loads the tile's key scales
+constexpr int kSplits = 4;                       // fp8 pieces of u
+constexpr int kE4m3Max = 448;
 
 struct IndexerParams {
   const uint8_t* q;        // [B, S1, 64, 128] fp8
@@ -55,9 +70,38 @@ __device__ __forceinline__ int visible_keys(int t, int aq, int ak, int sparse_mo
   return ak;
 }
 
+__device__ __forceinline__ float fp8_to_f32(uint32_t byte) {
+  return __builtin_amdgcn_cvt_f32_fp8((int)byte, 0);
+}
+
+// Waits until at most n of this wave's vector-memory operations are in flight
+// (n is a small run-time value; each case is an immediate s_waitcnt).
+__device__ __forceinline__ void wait_vmcnt_upto(int n) {
+  switch (n) {
+    case 0: dsa::wait_vmcnt<0>(); break;
+    case 1: dsa::wait_vmcnt<1>(); break;
+    case 2: dsa::wait_vmcnt<2>(); break;
+    case 3: dsa::wait_vmcnt<3>(); break;
+    case 4: dsa::wait_vmcnt<4>(); break;
+    default: dsa::wait_vmcnt<5>(); break;
+  }
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)(const DSA_LDS unsigned char*)p;
+}
+
+template <int OFF>
+__device__ __forceinline__ float lds_read_f32(uint32_t addr) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+
 __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) {
-  __shared__ __align__(16) uint8_t ktile[2][kKeyTile * kRowBytes];
-  __shared__ float kscale[2][kKeyTile];
+  __shared__ __align__(1024) uint8_t ktile[kStages][kTileBytes];
+  __shared__ __align__(256) float kscale[kStages][kKeyTile];
+  __shared__ __align__(16) uint8_t usplit[kWaves][kSplits][kDim];
 
   // XCD-aware mapping: key groups (b, chunk) are dealt to XCDs, all token blocks
   // of one key group run on the same XCD.
@@ -71,12 +115,12 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   const int aq = p.act_q ? clampi(p.act_q[b], 0, p.S1) : p.S1;
   const int ak = p.act_k ? clampi(p.act_k[b], 0, p.S2) : p.S2;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
 
   // Key range of this workgroup: its chunk, clipped to what its tokens can see.
   int lmax = 0;
-#pragma unroll
   for (int i = 0; i < kTokPerBlock; ++i) {
     const int t = tb * kTokPerBlock + i;
     if (t < p.S1) lmax = max(lmax, visible_keys(t, aq, ak, p.sparse_mode));
@@ -85,113 +129,176 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   const int kend = min(k0 + p.chunk, p.S2);  // last key this workgroup may write
   const int k1 = min(kend, lmax);            // last key any token needs
 
-  int tok[kTokPerWave], L[kTokPerWave];
-#pragma unroll
-  for (int j = 0; j < kTokPerWave; ++j) {
-    tok[j] = tb * kTokPerBlock + wave * kTokPerWave + j;
-    L[j] = tok[j] < p.S1 ? visible_keys(tok[j], aq, ak, p.sparse_mode) : 0;
-  }
-  if (kc == 0 && p.row_len != nullptr && lane == 0) {
-#pragma unroll
-    for (int j = 0; j < kTokPerWave; ++j)
-      if (tok[j] < p.S1) p.row_len[(int64_t)b * p.S1 + tok[j]] = L[j];
-  }
+  const int tok = tb * kTokPerBlock + wave;
+  const bool tok_ok = tok < p.S1;
+  const int L = tok_ok ? visible_keys(tok, aq, ak, p.sparse_mode) : 0;
+  if (kc == 0 && p.row_len != nullptr && lane == 0 && tok_ok) p.row_len[(int64_t)b * p.S1 + tok] = L;
   if (k0 >= k1) return;
+  const int64_t trow = (int64_t)b * p.S1 + (tok_ok ? tok : 0);
 
-  // A operands: lane (g, c) holds head 16*mt + c, bytes [32g, 32g+32) of the head.
-  dsa::i32x8 qa[kTokPerWave][4];
-  float wt[kTokPerWave][4][4];
+  // ---- per-token operands -------------------------------------------------
+  // q: lane (g, c) holds head 16*mt + c, bytes [32g, 32g+32) of the head.
+  dsa::i32x8 qa[4];
 #pragma unroll
-  for (int j = 0; j < kTokPerWave; ++j) {
-    const bool ok = tok[j] < p.S1;
-    const int64_t trow = (int64_t)b * p.S1 + (ok ? tok[j] : 0);
+  for (int mt = 0; mt < 4; ++mt) {
+    const dsa::i32x4* src =
+        reinterpret_cast<const dsa::i32x4*>(p.q + (trow * kHeads + 16 * mt + c) * kDim + 32 * g);
+    const dsa::i32x4 lo = tok_ok ? src[0] : dsa::i32x4{0, 0, 0, 0};
+    const dsa::i32x4 hi = tok_ok ? src[1] : dsa::i32x4{0, 0, 0, 0};
+    qa[mt] = dsa::i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  // w/2 for the heads whose |q.k| this lane's accumulators hold (16mt + 4g + i).
+  float wh[4][4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const dsa::i32x4* src =
-          reinterpret_cast<const dsa::i32x4*>(p.q + (trow * kHeads + 16 * mt + c) * kDim + 32 * g);
-      dsa::i32x4 lo = ok ? src[0] : dsa::i32x4{0, 0, 0, 0};
-      dsa::i32x4 hi = ok ? src[1] : dsa::i32x4{0, 0, 0, 0};
-      qa[j][mt] = dsa::i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) wt[j][mt][i] = ok ? p.w[trow * kHeads + 16 * mt + 4 * g + i] : 0.f;
+    for (int i = 0; i < 4; ++i) wh[mt][i] = tok_ok ? 0.5f * p.w[trow * kHeads + 16 * mt + 4 * g + i] : 0.f;
+
+  // u/2 = sum_h (w_h / 2) q_h: lane l computes dims 2l and 2l+1.
+  float u0 = 0.f, u1 = 0.f;
+  if (tok_ok) {
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(p.q + trow * kHeads * kDim) + lane;
+    const float* wrow = p.w + trow * kHeads;
+#pragma unroll 8
+    for (int h = 0; h < kHeads; ++h) {
+      const uint32_t two = qrow[h * (kDim / 2)];
+      const float wv = 0.5f * wrow[h];
+      u0 = fmaf(wv, fp8_to_f32(two & 0xff), u0);
+      u1 = fmaf(wv, fp8_to_f32(two >> 8), u1);
     }
   }
-
-  // Staging: thread tid copies 16 bytes of key (tid / 8), part (tid % 8).
-  const int skey = tid >> 3, spart = tid & 7;
-  const uint8_t* kbase = p.k + (int64_t)b * p.S2 * kDim;
-  const float* sbase = p.key_scale ? p.key_scale + (int64_t)b * p.S2 : nullptr;
-  auto load_tile = [&](int kt0, dsa::i32x4& v, float& sc) {
-    const int key = kt0 + skey;
-    v = key < k1 ? *reinterpret_cast<const dsa::i32x4*>(kbase + (int64_t)key * kDim + spart * 16)
-                 : dsa::i32x4{0, 0, 0, 0};
-    sc = 1.f;
-    if (tid < kKeyTile) {
-      const int key2 = kt0 + tid;
-      sc = (sbase && key2 < k1) ? sbase[key2] : 1.f;
-    }
-  };
-  auto store_tile = [&](int buf, const dsa::i32x4& v, float sc) {
-    *reinterpret_cast<dsa::i32x4*>(&ktile[buf][skey * kRowBytes + spart * 16]) = v;
-    if (tid < kKeyTile) kscale[buf][tid] = sc;
-  };
-
-  const int ntiles = (k1 - k0 + kKeyTile - 1) / kKeyTile;
+  // Power-of-two split of u: sigma_s = 2^(e - 4s) with max|u| / 2^e in (224, 448].
+  float umax = fmaxf(fabsf(u0), fabsf(u1));
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) umax = fmaxf(umax, __shfl_xor(umax, d, 64));
+  int e = -100;
+  if (umax > 0.f) {
+    int ex;
+    (void)frexpf(umax / (float)kE4m3Max, &ex);  // umax/448 = f * 2^ex, f in [0.5, 1)
+    e = clampi(ex, -100, 100);
+  }
   {
-    dsa::i32x4 v;
-    float sc;
-    load_tile(k0, v, sc);
-    store_tile(0, v, sc);
+    float r0 = u0, r1 = u1;
+#pragma unroll
+    for (int sp = 0; sp < kSplits; ++sp) {
+      const float inv = ldexpf(1.f, 4 * sp - e), sig = ldexpf(1.f, e - 4 * sp);
+      const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(r0 * inv, r1 * inv, 0, false);
+      *reinterpret_cast<uint16_t*>(&usplit[wave][sp][2 * lane]) = (uint16_t)pk;
+      r0 = fmaf(-sig, __builtin_amdgcn_cvt_f32_fp8(pk, 0), r0);
+      r1 = fmaf(-sig, __builtin_amdgcn_cvt_f32_fp8(pk, 1), r1);
+    }
   }
   __syncthreads();
+  // u pieces as A rows 0, 4, 8, 12 (piece g in the rows of lane group g), bytes 32g..32g+31.
+  dsa::i32x8 ua = {0, 0, 0, 0, 0, 0, 0, 0};
+  int uscale = 127;
+  if ((c & 3) == 0) {
+    const int sp = c >> 2;
+    const dsa::i32x4* src = reinterpret_cast<const dsa::i32x4*>(&usplit[wave][sp][32 * g]);
+    const dsa::i32x4 lo = src[0], hi = src[1];
+    ua = dsa::i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    uscale = clampi(127 + e - 4 * sp, 1, 254);
+  }
+
+  // ---- key tiles ------------------------------------------------------------
+  const int ntiles = (k1 - k0 + kKeyTile - 1) / kKeyTile;
+  const uint8_t* kbase = p.k + (int64_t)b * p.S2 * kDim;
+  const float* sbase = p.key_scale ? p.key_scale + (int64_t)b * p.S2 : nullptr;
+  const bool loader = wave < kKeyLoaders || (wave == kScaleLoader && sbase != nullptr);
+  // Loader lane l of wave w fills LDS bytes [w KB + 16 l, +16) of a tile: key
+  // s = 8w + l/8, slot l%8, which holds the key's chunk (l%8) ^ (s%8).
+  const int lkey = 8 * wave + (lane >> 3);
+  const int lchunk = (lane & 7) ^ ((lane >> 3) & 7);
+  auto issue = [=](int tile) {
+    const int t = tile < ntiles ? tile : ntiles - 1;  // past the end: reload the last tile (never read)
+    const int kt0 = k0 + t * kKeyTile;
+    if (wave < kKeyLoaders) {
+      const int key = min(kt0 + lkey, k1 - 1);
+      __builtin_amdgcn_global_load_lds(kbase + (int64_t)key * kDim + 16 * lchunk,
+                                       (DSA_LDS void*)&ktile[t & (kStages - 1)][1024 * wave], 16, 0, 0);
+    } else if (wave == kScaleLoader && sbase != nullptr) {
+      const int key = min(kt0 + lane, k1 - 1);
+      __builtin_amdgcn_global_load_lds(sbase + key, (DSA_LDS void*)&kscale[t & (kStages - 1)][0], 4, 0, 0);
+    }
+  };
+  // B-operand reads: lane (g, c) reads key 16blk + c, chunks 2g and 2g+1.
+  const int rslot = (2 * g) ^ (c & 7);
+  const uint32_t rd0 = lds_addr(&ktile[0][0]) + c * kDim + 16 * rslot;
+  const uint32_t rd1 = lds_addr(&ktile[0][0]) + c * kDim + 16 * (rslot ^ 1);
+  const uint32_t sc_addr = lds_addr(&kscale[0][0]) + 4 * lane;
+
+  // Logit stores: a buffer descriptor over this row's part of the chunk; stores
+  // past it (keys >= kend, or an out-of-range token) are dropped by the hardware,
+  // so every wave issues exactly one store per tile.
+  float* orow = p.logits + trow * p.ld + k0;
+  const __amdgpu_buffer_rsrc_t ost = __builtin_amdgcn_make_buffer_rsrc(
+      orow, (short)0, tok_ok ? (kend - k0) * 4 : 0, 0x00020000);
+
+  // The operand loads above complete before the ring starts, so the only vector
+  // memory operations in flight inside the loop are the ring's and the stores.
+  dsa::wait_vmcnt<0>();
+#pragma unroll
+  for (int i = 0; i < kStages - 1; ++i) issue(i);
 
   const dsa::f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    const int kt0 = k0 + it * kKeyTile;
-    dsa::i32x4 nv;
-    float nsc;
-    const bool more = it + 1 < ntiles;
-    if (more) load_tile(kt0 + kKeyTile, nv, nsc);
+    // This wave's load of tile `it` is done once at most min(2 + it, 5) newer
+    // memory operations (loads of later tiles, logit stores) are in flight.
+    if (loader) wait_vmcnt_upto(min(kStages - 2 + it, 2 * kStages - 3));
+    __builtin_amdgcn_s_barrier();
+    issue(it + kStages - 1);
 
-    float res[kTokPerWave][4];
+    const int st = it & (kStages - 1);
+    const uint32_t so = st * kTileBytes;
+    float a[4];
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
-      const uint8_t* rp = &ktile[buf][(blk * 16 + c) * kRowBytes + 32 * g];
-      const dsa::i32x4 b0 = *reinterpret_cast<const dsa::i32x4*>(rp);
-      const dsa::i32x4 b1 = *reinterpret_cast<const dsa::i32x4*>(rp + 16);
+      dsa::i32x4 b0, b1;
+      switch (blk) {  // immediate offsets: 16 keys x 128 B per block
+        case 0: b0 = dsa::lds_read_b128<0>(rd0 + so); b1 = dsa::lds_read_b128<0>(rd1 + so); break;
+        case 1: b0 = dsa::lds_read_b128<2048>(rd0 + so); b1 = dsa::lds_read_b128<2048>(rd1 + so); break;
+        case 2: b0 = dsa::lds_read_b128<4096>(rd0 + so); b1 = dsa::lds_read_b128<4096>(rd1 + so); break;
+        default: b0 = dsa::lds_read_b128<6144>(rd0 + so); b1 = dsa::lds_read_b128<6144>(rd1 + so); break;
+      }
+      dsa::lds_wait1<0>(b0);
+      dsa::lds_wait1<0>(b1);
       const dsa::i32x8 bf = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+      dsa::f32x4 d[4];
 #pragma unroll
-      for (int j = 0; j < kTokPerWave; ++j) {
-        float acc = 0.f;
+      for (int mt = 0; mt < 4; ++mt)  // D[row = head 16mt + 4g + i][col = key 16blk + c]
+        d[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[mt], bf, zero, 0, 0, 0, 127, 0, 127);
+      const dsa::f32x4 du = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ua, bf, zero, 0, 0, 0, uscale, 0, 127);
+      float acc = du[0];  // row 4g: piece g of u/2 . k
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          // D[row = head 16mt + 4g + i][col = key blk*16 + c]
-          const dsa::f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              qa[j][mt], bf, zero, 0, 0, 0, 127, 0, 127);
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc = fmaf(wt[j][mt][i], fmaxf(d[i], 0.f), acc);
-        }
-        acc += __shfl_xor(acc, 16, 64);
-        acc += __shfl_xor(acc, 32, 64);
-        res[j][blk] = acc;
-      }
+        for (int i = 0; i < 4; ++i) acc = fmaf(wh[mt][i], fabsf(d[mt][i]), acc);
+      a[blk] = acc;
     }
+    // Reduce-scatter over the 4 lane groups: afterwards lane group g holds the
+    // full sum of block g, i.e. lane l the logit of key 64-tile + l.
+    float r02, r13;
+    {
+      const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[0]), __float_as_uint(a[2]), false, false);
+      r02 = __uint_as_float(s0[0]) + __uint_as_float(s0[1]);
+      const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[1]), __float_as_uint(a[3]), false, false);
+      r13 = __uint_as_float(s1[0]) + __uint_as_float(s1[1]);
+    }
+    const auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(r02), __float_as_uint(r13), false, false);
+    const float sum = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
 
-    // lane (g, c) writes key kt0 + 16g + c
-    const int s = kt0 + lane;
-    const float sc = kscale[buf][lane];
-#pragma unroll
-    for (int j = 0; j < kTokPerWave; ++j) {
-      if (tok[j] < p.S1 && s < kend) {
-        float v = g == 0 ? res[j][0] : (g == 1 ? res[j][1] : (g == 2 ? res[j][2] : res[j][3]));
-        v = s < L[j] ? v * sc : -__builtin_inff();
-        __builtin_nontemporal_store(v, p.logits + ((int64_t)b * p.S1 + tok[j]) * p.ld + s);
-      }
+    const int kt0 = k0 + it * kKeyTile;
+    const int key = kt0 + lane;
+    float ks = 1.f;
+    if (sbase != nullptr) {
+      ks = lds_read_f32<0>(sc_addr + st * (kKeyTile * 4));
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ks));
     }
-    if (more) store_tile(buf ^ 1, nv, nsc);
-    __syncthreads();
+    const float v = key < L ? sum * ks : -__builtin_inff();
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ost, (kt0 - k0 + lane) * 4, 0, 0);
   }
+  // No LDS DMA may still be in flight when the workgroup's LDS is released.
+  if (loader) dsa::wait_vmcnt<0>();
 }
 
 }  // namespace

@@ -45,7 +45,6 @@ constexpr float kSlack = 8.f;    // log2 headroom of the reference maximum
 
 typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short i16x8;
-#define DSA_LDS __attribute__((address_space(3)))
 
 struct MlaParams {
   const uint16_t* q;            // [T, H, Dqk]
@@ -68,74 +67,17 @@ struct MlaParams {
   int causal;
 };
 
-// s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
-
-// Transposing LDS read (ds_read_b64_tr_b16) issued as inline asm.  The builtin
-// form makes the compiler drain every in-flight global_load_lds (vmcnt(0))
-// before it, since it cannot tell the two apart; here the caller orders the
-// read after the step's barrier and waits for its result with lds_wait<N>.
-template <int OFF>
-__device__ __forceinline__ dsa::i32x2 lds_read_tr16(uint32_t addr) {
-  dsa::i32x2 v;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
-  return v;
-}
-// 16-byte LDS read issued as inline asm, for the same reason: it pins how far
-// ahead of their MFMAs the reads run.
-template <int OFF>
-__device__ __forceinline__ dsa::i32x4 lds_read_b128(uint32_t addr) {
-  dsa::i32x4 v;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
-  return v;
-}
-template <int N>
-__device__ __forceinline__ void lds_wait1(dsa::i32x4& a) {
-  static_assert(N >= 0 && N < 16, "lgkmcnt range");
-  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "i"(N));
-}
-// s_waitcnt lgkmcnt(N); the registers passed in are tied to the wait so that no
-// use of them is scheduled before it.
-template <int N>
-__device__ __forceinline__ void lds_wait(dsa::i32x2& a, dsa::i32x2& b) {
-  static_assert(N >= 0 && N < 16, "lgkmcnt range");
-  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
-}
-
-template <int V>
-struct IntC {
-  static constexpr int value = V;
-};
-// Compile-time loop: f(IntC<B>{}), ..., f(IntC<E - 1>{}).
-template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(IntC<B>{});
-    static_for<B + 1, E>(f);
-  }
-}
-
-// Cross-lane reductions over the lane groups l ^ 16 and l ^ 32 (gfx950 permlane swaps).
-__device__ __forceinline__ float xor16_max(float x) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xor32_max(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xor16_sum(float x) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float xor32_sum(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
+using dsa::IntC;
+using dsa::lds_read_b128;
+using dsa::lds_read_tr16;
+using dsa::lds_wait;
+using dsa::lds_wait1;
+using dsa::static_for;
+using dsa::wait_vmcnt;
+using dsa::xor16_max;
+using dsa::xor16_sum;
+using dsa::xor32_max;
+using dsa::xor32_sum;
 
 // Source of the gathers for invalid keys: always in bounds, always zero.
 __device__ __align__(16) uint16_t g_zero_row[576];
