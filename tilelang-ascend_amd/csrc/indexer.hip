@@ -10,22 +10,27 @@
 //
 // Formulation.  ReLU(d) = (d + |d|) / 2, so with u_t = sum_h w[t, h] q[t, h, :]
 //   sum_h w_h ReLU(q_h . k) = ( sum_h w_h |q_h . k|  +  u_t . k ) / 2.
-// The first sum costs one FMA per (head, key) with the |.| source modifier; the
-// second is one more fp8 MFMA per 16 keys whose A rows hold u_t split into four
-// fp8 pieces with power-of-two scales (E8M0 block scales of the MFMA):
-// u = sum_s 2^(e-4s) u_s, exact to 2^-17 of max|u|.  Both terms keep fp32-level
-// accuracy; no rounding of q.k to a narrower type takes place.
+// The first sum costs one FMA per (head, key) with the |.| source modifier.  The
+// second is an fp8 MFMA whose A rows hold u split into four fp8 pieces with
+// power-of-two scales (E8M0 block scales of the MFMA), u = sum_s 2^(e-4s) u_s,
+// exact to 2^-17 of max|u|; its 16 rows carry the pieces of 4 tokens, so one
+// MFMA per 16 keys serves 4 waves.  Both terms keep fp32-level accuracy; q.k is
+// never rounded to a narrower type.
 //
 // Work decomposition.  One workgroup = 16 waves = 16 query tokens (one per wave)
 // of one batch row x one chunk of keys.  A wave holds its token's A operands
 // (64 heads x 128 dims of fp8 plus the u pieces) in registers.  K streams through
 // a 4-stage LDS ring of 64-key tiles filled with global_load_lds (three tiles in
 // flight while one is computed); a tile stores 16-byte chunk j of key s at slot
-// j ^ (s & 7) so the B-operand reads are free of bank conflicts.  Per 16-key block
-// a wave issues 5 fp8 MFMAs (v_mfma_scale_f32_16x16x128_f8f6f4) and 17 VALU ops;
-// the 4 lane groups then exchange their partial sums with permlane swaps (a
-// reduce-scatter) so that lane l ends up with key 64-tile + l and the whole tile
-// is one coalesced 256-byte store.  Workgroups that share a key chunk are placed
+// j ^ (s & 7) ^ ((s >> 3) & 1), which keeps the B-operand reads (16 keys x one
+// chunk, 128-byte rows) on distinct banks for both 8- and 16-lane LDS phases.  Per 16-key block
+// a wave issues 4 fp8 MFMAs (v_mfma_scale_f32_16x16x128_f8f6f4) and 16 FMAs, and
+// once per tile the u MFMA for one block of its group of 4 waves (the results
+// pass through LDS).  The 4 lane groups then exchange their partial sums with
+// permlane swaps (a reduce-scatter) so that lane l ends up with key 64-tile + l
+// and the tile is one coalesced 256-byte store.  That epilogue of tile i runs in
+// iteration i+1, behind the first MFMAs of tile i+1, so the waves released by a
+// barrier start with matrix work rather than all doing VALU work at once.  Workgroups that share a key chunk are placed
 // on the same XCD so the chunk stays in that XCD's L2.
 #include "dsa_common.h"
 
@@ -91,6 +96,12 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(size_t)(const DSA_LDS unsigned char*)p;
 }
 
+// s_waitcnt lgkmcnt(N) tied to both halves of a B fragment.
+template <int N>
+__device__ __forceinline__ void lds_wait2(dsa::i32x4& a, dsa::i32x4& b) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+
 template <int OFF>
 __device__ __forceinline__ float lds_read_f32(uint32_t addr) {
   float v;
@@ -101,7 +112,11 @@ __device__ __forceinline__ float lds_read_f32(uint32_t addr) {
 __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) {
   __shared__ __align__(1024) uint8_t ktile[kStages][kTileBytes];
   __shared__ __align__(256) float kscale[kStages][kKeyTile];
-  __shared__ __align__(16) uint8_t usplit[kWaves][kSplits][kDim];
+  // u pieces, rows padded to 144 B so the 16 rows one MFMA operand read touches
+  // fall on distinct banks
+  __shared__ __align__(16) uint8_t usplit[kWaves][kSplits][kDim + 16];
+  __shared__ int uexp[kWaves];
+  __shared__ __align__(16) float lin[2][kWaves][kKeyTile];  // u.k per token and key, two tiles
 
   // XCD-aware mapping: key groups (b, chunk) are dealt to XCDs, all token blocks
   // of one key group run on the same XCD.
@@ -177,6 +192,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
     (void)frexpf(umax / (float)kE4m3Max, &ex);  // umax/448 = f * 2^ex, f in [0.5, 1)
     e = clampi(ex, -100, 100);
   }
+  if (lane == 0) uexp[wave] = e;
   {
     float r0 = u0, r1 = u1;
 #pragma unroll
@@ -189,16 +205,13 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
     }
   }
   __syncthreads();
-  // u pieces as A rows 0, 4, 8, 12 (piece g in the rows of lane group g), bytes 32g..32g+31.
-  dsa::i32x8 ua = {0, 0, 0, 0, 0, 0, 0, 0};
-  int uscale = 127;
-  if ((c & 3) == 0) {
-    const int sp = c >> 2;
-    const dsa::i32x4* src = reinterpret_cast<const dsa::i32x4*>(&usplit[wave][sp][32 * g]);
-    const dsa::i32x4 lo = src[0], hi = src[1];
-    ua = dsa::i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    uscale = clampi(127 + e - 4 * sp, 1, 254);
-  }
+  // u pieces of the group's 4 tokens as A rows: row 4*tq + sp = piece sp of token
+  // grp0 + tq; lane (g, c) holds row c, bytes 32g..32g+31.  In the result, lane
+  // (g, c) then holds the 4 pieces (rows 4g..4g+3) of token grp0 + g for key c.
+  // The operand stays in LDS (read once per tile, where it is used).
+  const int grp0 = wave & ~3, ublk = wave & 3;
+  const uint32_t ua_addr = lds_addr(&usplit[grp0 + (c >> 2)][c & 3][32 * g]);
+  const int uscale = clampi(127 + uexp[grp0 + (c >> 2)] - 4 * (c & 3), 1, 254);
 
   // ---- key tiles ------------------------------------------------------------
   const int ntiles = (k1 - k0 + kKeyTile - 1) / kKeyTile;
@@ -206,9 +219,9 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   const float* sbase = p.key_scale ? p.key_scale + (int64_t)b * p.S2 : nullptr;
   const bool loader = wave < kKeyLoaders || (wave == kScaleLoader && sbase != nullptr);
   // Loader lane l of wave w fills LDS bytes [w KB + 16 l, +16) of a tile: key
-  // s = 8w + l/8, slot l%8, which holds the key's chunk (l%8) ^ (s%8).
+  // s = 8w + l/8, slot l%8, which holds the key's chunk (l%8) ^ swz(s).
   const int lkey = 8 * wave + (lane >> 3);
-  const int lchunk = (lane & 7) ^ ((lane >> 3) & 7);
+  const int lchunk = (lane & 7) ^ (lkey & 7) ^ ((lkey >> 3) & 1);
   auto issue = [=](int tile) {
     const int t = tile < ntiles ? tile : ntiles - 1;  // past the end: reload the last tile (never read)
     const int kt0 = k0 + t * kKeyTile;
@@ -222,10 +235,11 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
     }
   };
   // B-operand reads: lane (g, c) reads key 16blk + c, chunks 2g and 2g+1.
-  const int rslot = (2 * g) ^ (c & 7);
+  const int rslot = (2 * g) ^ (c & 7) ^ (c >> 3);
   const uint32_t rd0 = lds_addr(&ktile[0][0]) + c * kDim + 16 * rslot;
   const uint32_t rd1 = lds_addr(&ktile[0][0]) + c * kDim + 16 * (rslot ^ 1);
   const uint32_t sc_addr = lds_addr(&kscale[0][0]) + 4 * lane;
+  const uint32_t ub_rd0 = rd0 + (wave & 3) * 2048, ub_rd1 = rd1 + (wave & 3) * 2048;  // block ublk
 
   // Logit stores: a buffer descriptor over this row's part of the chunk; stores
   // past it (keys >= kend, or an out-of-range token) are dropped by the hardware,
@@ -240,62 +254,116 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
 #pragma unroll
   for (int i = 0; i < kStages - 1; ++i) issue(i);
 
+  // u.k hand-off: this wave writes block ublk of its group's 4 tokens, reads its own token.
+  const uint32_t lin_wr = lds_addr(&lin[0][grp0 + g][16 * ublk + c]);
+  const uint32_t lin_rd = lds_addr(&lin[0][wave][lane]);
+  constexpr uint32_t kLinBuf = kWaves * kKeyTile * 4;
+
+  // Epilogue of a finished tile: reduce-scatter of the partial sums, plus u.k,
+  // times the key scale, masked, stored.  tile < 0 issues a store that the
+  // buffer range check drops, so every iteration has exactly one store.
+  auto finish = [&](const float (&ap)[4], float ksp, int tile, auto LB) {
+    constexpr uint32_t lin_off = decltype(LB)::value * kLinBuf;
+    float r02, r13;
+    {
+      const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ap[0]), __float_as_uint(ap[2]), false, false);
+      r02 = __uint_as_float(s0[0]) + __uint_as_float(s0[1]);
+      const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ap[1]), __float_as_uint(ap[3]), false, false);
+      r13 = __uint_as_float(s1[0]) + __uint_as_float(s1[1]);
+    }
+    const auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(r02), __float_as_uint(r13), false, false);
+    float sum = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
+    int voff = 0x40000000;  // beyond any descriptor range: dropped
+    if (tile >= 0) {
+      float lk = lds_read_f32<lin_off>(lin_rd);
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lk));
+      sum += lk;
+      const int key = k0 + tile * kKeyTile + lane;
+      sum = key < L ? sum * ksp : -__builtin_inff();
+      voff = (tile * kKeyTile + lane) * 4;
+    }
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sum), ost, voff, 0, 0);
+  };
+
   const dsa::f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  for (int it = 0; it < ntiles; ++it) {
+  float ap[4] = {0.f, 0.f, 0.f, 0.f};
+  float ksp = 1.f;
+  // One tile; ST = it % kStages is a compile-time ring slot, so every LDS offset
+  // below is an instruction immediate.
+  auto step = [&](int it, auto STC) {
+    constexpr int ST = decltype(STC)::value;
+    constexpr uint32_t so = ST * kTileBytes;
     // This wave's load of tile `it` is done once at most min(2 + it, 5) newer
-    // memory operations (loads of later tiles, logit stores) are in flight.
+    // memory operations (loads of later tiles, logit stores) are in flight; its
+    // LDS writes and reads of the previous iteration are complete.
     if (loader) wait_vmcnt_upto(min(kStages - 2 + it, 2 * kStages - 3));
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ksp));
     __builtin_amdgcn_s_barrier();
+    // The four waves of a SIMD are served oldest-first; a wave lowers its priority
+    // as it gets through the tile, so the four finish the tile together instead
+    // of the oldest idling at the next barrier while the youngest runs alone.
+    __builtin_amdgcn_s_setprio(3);
     issue(it + kStages - 1);
 
-    const int st = it & (kStages - 1);
-    const uint32_t so = st * kTileBytes;
+    float ksc = 1.f;
+    if (sbase != nullptr) ksc = lds_read_f32<ST * kKeyTile * 4>(sc_addr);
     float a[4];
-#pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
-      dsa::i32x4 b0, b1;
-      switch (blk) {  // immediate offsets: 16 keys x 128 B per block
-        case 0: b0 = dsa::lds_read_b128<0>(rd0 + so); b1 = dsa::lds_read_b128<0>(rd1 + so); break;
-        case 1: b0 = dsa::lds_read_b128<2048>(rd0 + so); b1 = dsa::lds_read_b128<2048>(rd1 + so); break;
-        case 2: b0 = dsa::lds_read_b128<4096>(rd0 + so); b1 = dsa::lds_read_b128<4096>(rd1 + so); break;
-        default: b0 = dsa::lds_read_b128<6144>(rd0 + so); b1 = dsa::lds_read_b128<6144>(rd1 + so); break;
+    // B fragments of block blk (16 keys x 128 B); the next block's read is in
+    // flight while the current block's MFMAs run.
+    dsa::i32x4 nb0 = dsa::lds_read_b128<so>(rd0), nb1 = dsa::lds_read_b128<so>(rd1);
+    dsa::static_for<0, 4>([&](auto BLK) {
+      constexpr int blk = decltype(BLK)::value;
+      dsa::i32x4 b0 = nb0, b1 = nb1;
+      if constexpr (blk < 3) {
+        nb0 = dsa::lds_read_b128<so + (blk + 1) * 2048>(rd0);
+        nb1 = dsa::lds_read_b128<so + (blk + 1) * 2048>(rd1);
+        lds_wait2<2>(b0, b1);
+      } else {
+        lds_wait2<0>(b0, b1);
       }
-      dsa::lds_wait1<0>(b0);
-      dsa::lds_wait1<0>(b1);
       const dsa::i32x8 bf = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
       dsa::f32x4 d[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)  // D[row = head 16mt + 4g + i][col = key 16blk + c]
         d[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[mt], bf, zero, 0, 0, 0, 127, 0, 127);
-      const dsa::f32x4 du = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ua, bf, zero, 0, 0, 0, uscale, 0, 127);
-      float acc = du[0];  // row 4g: piece g of u/2 . k
+      if constexpr (blk == 0) finish(ap, ksp, it - 1, dsa::IntC<(ST + 1) & 1>{});
+      float acc = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc = fmaf(wh[mt][i], fabsf(d[mt][i]), acc);
       a[blk] = acc;
-    }
-    // Reduce-scatter over the 4 lane groups: afterwards lane group g holds the
-    // full sum of block g, i.e. lane l the logit of key 64-tile + l.
-    float r02, r13;
+      __builtin_amdgcn_s_setprio(blk < 2 ? 2 - blk : 0);
+    });
     {
-      const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[0]), __float_as_uint(a[2]), false, false);
-      r02 = __uint_as_float(s0[0]) + __uint_as_float(s0[1]);
-      const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[1]), __float_as_uint(a[3]), false, false);
-      r13 = __uint_as_float(s1[0]) + __uint_as_float(s1[1]);
+      // u.k of block ublk for the group's 4 tokens -> LDS (read in the next iteration).
+      dsa::i32x4 u0 = dsa::lds_read_b128<0>(ua_addr), u1 = dsa::lds_read_b128<16>(ua_addr);
+      dsa::i32x4 k0v = dsa::lds_read_b128<so>(ub_rd0), k1v = dsa::lds_read_b128<so>(ub_rd1);
+      lds_wait2<0>(u0, u1);
+      lds_wait2<0>(k0v, k1v);
+      const dsa::i32x8 ua = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
+      const dsa::i32x8 ub = {k0v[0], k0v[1], k0v[2], k0v[3], k1v[0], k1v[1], k1v[2], k1v[3]};
+      const dsa::f32x4 du = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ua, ub, zero, 0, 0, 0, uscale, 0, 127);
+      const float lv = (du[0] + du[1]) + (du[2] + du[3]);
+      asm volatile("ds_write_b32 %0, %1 offset:%2" : : "v"(lin_wr), "v"(lv), "i"((ST & 1) * kLinBuf) : "memory");
     }
-    const auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(r02), __float_as_uint(r13), false, false);
-    const float sum = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
-
-    const int kt0 = k0 + it * kKeyTile;
-    const int key = kt0 + lane;
-    float ks = 1.f;
-    if (sbase != nullptr) {
-      ks = lds_read_f32<0>(sc_addr + st * (kKeyTile * 4));
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ks));
-    }
-    const float v = key < L ? sum * ks : -__builtin_inff();
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ost, (kt0 - k0 + lane) * 4, 0, 0);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) ap[blk] = a[blk];
+    ksp = ksc;
+  };
+  for (int it = 0; it < ntiles; it += kStages) {
+    step(it, dsa::IntC<0>{});
+    if (it + 1 < ntiles) step(it + 1, dsa::IntC<1>{});
+    if (it + 2 < ntiles) step(it + 2, dsa::IntC<2>{});
+    if (it + 3 < ntiles) step(it + 3, dsa::IntC<3>{});
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ksp));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_s_setprio(0);
+  {
+    const int last = ntiles - 1;
+    if (last & 1) finish(ap, ksp, last, dsa::IntC<1>{});
+    else finish(ap, ksp, last, dsa::IntC<0>{});
   }
   // No LDS DMA may still be in flight when the workgroup's LDS is released.
   if (loader) dsa::wait_vmcnt<0>();
