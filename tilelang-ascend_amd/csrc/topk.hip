@@ -13,17 +13,18 @@
 // top-K set is exactly {C >= C_K} for the K-th largest composite C_K.
 //
 // Selection.  C_K is found digit by digit (12-bit digits, LDS histograms).
-//  * Rows of up to 32K elements are held in registers and read from HBM once.
-//  * Longer rows: a sample of the row (64-element blocks spread over it) gives a
-//    threshold T whose estimated count above it is ~1.25 K; one vectorised pass
-//    then copies every element >= T into LDS.  If at least K and at most the LDS
+//  * Rows of up to 16K elements are held in registers and read from HBM once.
+//  * Rows of at least 8 K elements: a sample of the row (64-element blocks spread
+//    over it) gives a threshold T whose estimated count above it is ~1.25 K; one
+//    pass (over the registers, or a double-buffered vectorised stream for longer
+//    rows) then copies every element >= T into LDS.  If at least K and at most the LDS
 //    capacity landed there, the top K are exactly among them and the remaining
 //    digits are resolved in LDS; otherwise exact histogram passes over the row
 //    take over.
-// Ordering.  The K chosen composites are bitonic-sorted (descending) by 256
-// threads holding 8 (or 32) keys each: strides below 8 stay in registers,
-// strides up to 256 use VALU cross-lane exchanges (DPP, permlane swaps), only
-// the largest strides go through LDS (3 barriers for K = 2048).
+// Ordering.  The K chosen composites are bitonic-sorted (descending) by all
+// 1024 threads holding 2 (or 8) keys each: strides below that stay in registers,
+// strides up to 64 threads use VALU cross-lane exchanges (DPP, permlane swaps),
+// only the largest strides go through LDS.
 #include "dsa_common.h"
 
 namespace {
@@ -33,7 +34,7 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kHistBits = 12;
 constexpr int kBins = 1 << kHistBits;
 constexpr int kCandCap = 5888;     // LDS candidate capacity (46 KB; two blocks fit per CU)
-constexpr int kSortThreads = 256;
+constexpr int kSortThreads = kThreads;
 constexpr int kSampleBlocks = 128; // 64-element blocks sampled from a long row
 
 __device__ __forceinline__ uint32_t ordered_key(float f) {
@@ -58,8 +59,7 @@ __device__ __forceinline__ uint64_t high_bits(uint64_t C, int s) { return s >= 6
 struct Shared {
   uint32_t hist[kBins];
   uint32_t wsum[kWaves];
-  uint32_t nsel;
-  uint32_t ncand;
+  uint32_t cnt[2];  // [0]: entries in sel, [1]: entries in cand
   uint32_t res_bucket;
   uint32_t res_above;
   uint32_t res_count;
@@ -160,25 +160,27 @@ __device__ __forceinline__ uint64_t xor_lane64(uint64_t x, int lane) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-__device__ __forceinline__ void cmp_swap(uint64_t& a, uint64_t& b, bool desc) {
-  const uint64_t lo = a < b ? a : b, hi = a < b ? b : a;
-  a = desc ? hi : lo;
-  b = desc ? lo : hi;
+// After a compare-exchange the element keeps the larger key when keep_hi, else
+// the smaller: it takes the partner's key exactly when (v < partner) == keep_hi.
+__device__ __forceinline__ uint64_t exchange(uint64_t v, uint64_t pv, bool keep_hi) {
+  return (v < pv) == keep_hi ? pv : v;
 }
 
-// Bitonic sort (descending) of buf[0 .. EPT * 256) by the first 256 threads, each
-// holding EPT consecutive keys; xbuf (same size) is the LDS exchange area for the
-// strides that cross waves.  All threads of the block must call it.
-template <int EPT>
-__device__ void sort_desc(uint64_t* buf, uint64_t* xbuf) {
+// Bitonic sort (descending) of buf[0 .. EPT * 1024) by the 1024 threads, each
+// holding EPT consecutive keys; xbuf is the LDS exchange area for the strides
+// that cross waves.  With DOUBLE it holds 2 x the keys and its halves are used
+// alternately, so one barrier per such stage suffices; otherwise each stage
+// takes a second barrier before the area is rewritten.  All threads of the
+// block must call it.
+template <int EPT, bool DOUBLE>
+__device__ __forceinline__ void sort_desc(uint64_t* buf, uint64_t* xbuf) {
   constexpr int N = EPT * kSortThreads;
   const int t = threadIdx.x;
-  const bool act = t < kSortThreads;
+  const int lane = t & 63;
   uint64_t v[EPT];
-  if (act) {
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) v[j] = buf[t * EPT + j];
-  }
+  for (int j = 0; j < EPT; ++j) v[j] = buf[t * EPT + j];
+  int xsel = 0;  // which half of xbuf the next cross-wave stage writes
   static_for<1, 16>([&](auto SZ) {
     constexpr int lsize = decltype(SZ)::value;  // size = 2^lsize
     if constexpr ((1 << lsize) <= N) {
@@ -186,52 +188,41 @@ __device__ void sort_desc(uint64_t* buf, uint64_t* xbuf) {
       static_for<0, lsize>([&](auto ST) {
         constexpr int stride = size >> (1 + decltype(ST)::value);
         if constexpr (stride < EPT) {
-          if (act) {
 #pragma unroll
-            for (int j = 0; j < EPT; ++j) {
-              if ((j & stride) == 0) {
-                const bool desc = ((t * EPT + j) & size) == 0;
-                cmp_swap(v[j], v[j + stride], desc);
-              }
+          for (int j = 0; j < EPT; ++j) {
+            if ((j & stride) == 0) {
+              // pair (j, j + stride): the lower position keeps the larger key when descending
+              const bool desc = ((t * EPT + j) & size) == 0;
+              const uint64_t a = v[j], b = v[j + stride];
+              const bool sw = (a < b) == desc;
+              v[j] = sw ? b : a;
+              v[j + stride] = sw ? a : b;
             }
           }
         } else if constexpr (stride < EPT * 64) {
-          if (act) {
-            constexpr int d = stride / EPT;  // partner lane distance within the wave
-            const bool keep_hi = (((t * EPT) & stride) == 0) == (((t * EPT) & size) == 0);
-            const int lane = t & 63;
+          constexpr int d = stride / EPT;  // partner lane distance within the wave
+          const bool keep_hi = (((t * EPT) & stride) == 0) == (((t * EPT) & size) == 0);
 #pragma unroll
-            for (int j = 0; j < EPT; ++j) {
-              const uint64_t pv = xor_lane64<d>(v[j], lane);
-              const uint64_t hi = v[j] < pv ? pv : v[j], lo = v[j] < pv ? v[j] : pv;
-              v[j] = keep_hi ? hi : lo;
-            }
-          }
+          for (int j = 0; j < EPT; ++j) v[j] = exchange(v[j], xor_lane64<d>(v[j], lane), keep_hi);
         } else {
           constexpr int d = stride / EPT;  // partner thread distance (another wave)
-          if (act) {
+          uint64_t* xb = DOUBLE ? xbuf + xsel * N : xbuf;
+          xsel ^= 1;
 #pragma unroll
-            for (int j = 0; j < EPT; ++j) xbuf[t * EPT + j] = v[j];
-          }
+          for (int j = 0; j < EPT; ++j) xb[t * EPT + j] = v[j];
           __syncthreads();
-          if (act) {
-            const bool keep_hi = (((t * EPT) & stride) == 0) == (((t * EPT) & size) == 0);
+          const bool keep_hi = (((t * EPT) & stride) == 0) == (((t * EPT) & size) == 0);
 #pragma unroll
-            for (int j = 0; j < EPT; ++j) {
-              const uint64_t pv = xbuf[(t ^ d) * EPT + j];
-              const uint64_t hi = v[j] < pv ? pv : v[j], lo = v[j] < pv ? v[j] : pv;
-              v[j] = keep_hi ? hi : lo;
-            }
-          }
-          __syncthreads();
+          for (int j = 0; j < EPT; ++j) v[j] = exchange(v[j], xb[(t ^ d) * EPT + j], keep_hi);
+          // DOUBLE: the next cross-wave stage writes the other half, and its
+          // barrier orders this stage's reads before this half is reused
+          if constexpr (!DOUBLE) __syncthreads();
         }
       });
     }
   });
-  if (act) {
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) buf[t * EPT + j] = v[j];
-  }
+  for (int j = 0; j < EPT; ++j) buf[t * EPT + j] = v[j];
   __syncthreads();
 }
 
@@ -267,8 +258,8 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
     L = r < 0 ? 0 : (r < a.cols ? r : a.cols);
   }
   if (tid == 0) {
-    sh->nsel = 0u;
-    sh->ncand = 0u;
+    sh->cnt[0] = 0u;
+    sh->cnt[1] = 0u;
   }
   auto idx_of = [=](int e) -> uint32_t { return ir ? (uint32_t)ir[e] : (uint32_t)e; };
 
@@ -290,16 +281,20 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
       }
     } else {
       if ((reinterpret_cast<uintptr_t>(xr) & 15) == 0) {
-        constexpr int U = 4;  // float4 loads in flight per thread
+        // U float4 per thread per batch; the next batch's loads are issued
+        // before the current batch is processed.
+        constexpr int U = 4;
+        constexpr int kStep = 4 * kThreads * U;
         const int L4 = L & ~3;
-        for (int base = 4 * tid; base < L4; base += 4 * kThreads * U) {
-          dsa::f32x4 v[U];
+        auto load = [=](dsa::f32x4 (&v)[U], int base) {
 #pragma unroll
           for (int u = 0; u < U; ++u) {
             const int e = base + 4 * kThreads * u;
             v[u] = e < L4 ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e))
                           : dsa::f32x4{0.f, 0.f, 0.f, 0.f};
           }
+        };
+        auto consume = [=](const dsa::f32x4 (&v)[U], int base) {
 #pragma unroll
           for (int u = 0; u < U; ++u) {
             const int e = base + 4 * kThreads * u;
@@ -308,10 +303,82 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
               for (int q = 0; q < 4; ++q) f(ordered_key(v[u][q]), e + q);
             }
           }
+        };
+        dsa::f32x4 va[U], vb[U];
+        load(va, 4 * tid);
+        for (int base = 4 * tid; base < L4; base += 2 * kStep) {
+          if (base + kStep < L4) load(vb, base + kStep);
+          consume(va, base);
+          if (base + 2 * kStep < L4) load(va, base + 2 * kStep);
+          if (base + kStep < L4) consume(vb, base + kStep);
         }
         for (int e = L4 + tid; e < L; e += kThreads) f(ordered_key(xr[e]), e);
       } else {
         for (int e = tid; e < L; e += kThreads) f(ordered_key(xr[e]), e);
+      }
+    }
+  };
+
+  // visit the row in batches: g(k, e, ok) with arrays of the batch's keys, element
+  // indices and validity.  All lanes of a wave take part in every call (the loop
+  // bounds are wave-uniform), so g may use ballots.
+  auto for_each_batch = [=](auto&& g) {
+    if constexpr (ITEMS > 0) {
+      uint32_t kk[ITEMS];
+      int ee[ITEMS];
+      bool ok[ITEMS];
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j) {
+        ee[j] = j * kThreads + tid;
+        ok[j] = ee[j] < L;
+        kk[j] = keys[j];
+      }
+      g(kk, ee, ok);
+    } else {
+      constexpr int U = 4;
+      constexpr int kStep = 4 * kThreads * U;
+      const bool vec = (reinterpret_cast<uintptr_t>(xr) & 15) == 0;
+      const int L4 = vec ? (L & ~3) : 0;
+      const int wbase = 4 * (tid & ~63);  // this wave's first element in a batch
+      auto load = [=](dsa::f32x4 (&v)[U], int base) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int e = base + 4 * kThreads * u;
+          v[u] = e < L4 ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e))
+                        : dsa::f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      };
+      auto consume = [=](const dsa::f32x4 (&v)[U], int base) {
+        uint32_t kk[4 * U];
+        int ee[4 * U];
+        bool ok[4 * U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int e = base + 4 * kThreads * u + q;
+            ee[4 * u + q] = e;
+            ok[4 * u + q] = e < L4;
+            kk[4 * u + q] = ordered_key(v[u][q]);
+          }
+        g(kk, ee, ok);
+      };
+      dsa::f32x4 va[U], vb[U];
+      if (wbase < L4) load(va, 4 * tid);
+      for (int b0 = 0; wbase + b0 < L4; b0 += 2 * kStep) {
+        const bool more1 = wbase + b0 + kStep < L4, more2 = wbase + b0 + 2 * kStep < L4;
+        if (more1) load(vb, 4 * tid + b0 + kStep);
+        consume(va, 4 * tid + b0);
+        if (more2) load(va, 4 * tid + b0 + 2 * kStep);
+        if (more1) consume(vb, 4 * tid + b0 + kStep);
+      }
+      // the scalar tail (and unaligned rows): one element per lane per call
+      for (int e0 = L4; e0 < L; e0 += kThreads) {
+        const int e = e0 + tid;
+        uint32_t kk[1] = {e < L ? ordered_key(xr[e]) : 0u};
+        int ee[1] = {e};
+        bool ok[1] = {e < L};
+        g(kk, ee, ok);
       }
     }
   };
@@ -331,14 +398,16 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
     bool done = false;
     bool have_cand = false;
 
-    if constexpr (ITEMS == 0) {
+    {
       // ---- sampled threshold, then one pass collecting everything above it ----
-      uint32_t* samp = reinterpret_cast<uint32_t*>(cand);  // kSampleBlocks * 64 keys
-      constexpr int ns = kSampleBlocks * 64;
-      if (L >= 4 * ns) {
+      uint32_t* samp = reinterpret_cast<uint32_t*>(cand);  // up to kSampleBlocks * 64 keys
+      // nb blocks of 64, at most a quarter of the row
+      const int nb = (L / 256) < kSampleBlocks ? (L / 256) : kSampleBlocks;
+      const int ns = nb * 64;
+      if (L >= 8 * K && nb >= 16) {
         for (int i = tid; i < ns; i += kThreads) {
           const int blk = i >> 6;
-          const int start = (int)(((int64_t)blk * L / kSampleBlocks) & ~63);
+          const int start = (int)(((int64_t)blk * L / nb) & ~63);
           samp[i] = ordered_key(xr[start + (i & 63)]);
         }
         // rank of the threshold inside the sample: ~1.25 K + 64 expected above it
@@ -358,20 +427,37 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
         find_bucket(*sh, r2);
         const uint32_t T = (b1 << 20) | (sh->res_bucket << 8);
         __syncthreads();
-        for_each([=](uint32_t key, int e) {
-          if (key >= T) {
-            const uint32_t slot = atomicAdd(&sh->ncand, 1u);
-            if (slot < (uint32_t)kCandCap) cand[slot] = composite(key, idx_of(e));
+        // wave-aggregated append: slots from ballots, one LDS atomic per wave and batch
+        const int lane = tid & 63;
+        for_each_batch([=](const auto& kk, const auto& ee, const auto& ok) {
+          constexpr int NB = sizeof(kk) / sizeof(kk[0]);
+          uint32_t off[NB];
+          uint32_t tot = 0;
+#pragma unroll
+          for (int j = 0; j < NB; ++j) {
+            const uint64_t m = __ballot(ok[j] && kk[j] >= T);
+            off[j] = tot + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            tot += (uint32_t)__popcll(m);
+          }
+          if (tot != 0) {
+            uint32_t base = 0;
+            if (lane == 0) base = atomicAdd(&sh->cnt[1], tot);
+            base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+              const uint32_t slot = base + off[j];
+              if (ok[j] && kk[j] >= T && slot < (uint32_t)kCandCap) cand[slot] = composite(kk[j], idx_of(ee[j]));
+            }
           }
         });
         __syncthreads();
-        const uint32_t nc = sh->ncand;
+        const uint32_t nc = sh->cnt[1];
         __syncthreads();
         if (nc >= (uint32_t)K && nc <= (uint32_t)kCandCap) {
           // the top K all lie among the candidates: the group is all of them
           have_cand = true;
         } else if (tid == 0) {
-          sh->ncand = 0u;  // fall back to the exact passes below
+          sh->cnt[1] = 0u;  // fall back to the exact passes below
         }
         __syncthreads();
       }
@@ -416,15 +502,18 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
       for_each([=](uint32_t key, int e) {
         const uint64_t C = composite(key, idx_of(e));
         const uint64_t hi = high_bits(C, s);
-        if (hi > P || (done && hi == P)) {
-          sel[atomicAdd(&sh->nsel, 1u)] = C;
-        } else if (hi == P) {
-          cand[atomicAdd(&sh->ncand, 1u)] = C;
+        // strictly above -> sel (slot in [0, P2)), the group -> cand (slot P2 + i):
+        // one LDS pool indexed arithmetically
+        const bool to_sel = hi > P || (done && hi == P);
+        if (to_sel || hi == P) {
+          const int which = to_sel ? 0 : 1;
+          const uint32_t slot = atomicAdd(&sh->cnt[which], 1u);
+          sel[slot + (to_sel ? 0u : (uint32_t)P2)] = C;
         }
       });
       __syncthreads();
     }
-    const int ncand = (int)sh->ncand;
+    const int ncand = (int)sh->cnt[1];
 
     // ---- resolve the remaining digits inside the LDS candidate group ----
     // (composites are distinct, so the group shrinks to the single C_K by s == 0)
@@ -449,7 +538,7 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
     }
     for (int i = tid; i < ncand; i += kThreads) {
       const uint64_t C = cand[i];
-      if (high_bits(C, s) >= P) sel[atomicAdd(&sh->nsel, 1u)] = C;
+      if (high_bits(C, s) >= P) sel[atomicAdd(&sh->cnt[0], 1u)] = C;
     }
     __syncthreads();
     nsel_final = K;
@@ -458,7 +547,8 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
   if (a.sort) {
     for (int i = nsel_final + tid; i < P2; i += kThreads) sel[i] = 0ull;  // pad: smallest composite
     __syncthreads();
-    sort_desc<EPT>(sel, cand);
+    constexpr bool kDouble = (kCandCap > P2 ? kCandCap : P2) >= 2 * P2;
+    sort_desc<EPT, kDouble>(sel, cand);
   }
 
   int32_t* orow = a.out_idx + row * (int64_t)K;
@@ -494,8 +584,7 @@ int launch_items(const TopkArgs& a, int64_t rows, hipStream_t stream) {
   if (cols <= 4 * kThreads) return launch_rows<4, EPT>(a, rows, stream);
   if (cols <= 8 * kThreads) return launch_rows<8, EPT>(a, rows, stream);
   if (cols <= 16 * kThreads) return launch_rows<16, EPT>(a, rows, stream);
-  if (cols <= 32 * kThreads) return launch_rows<32, EPT>(a, rows, stream);
-  return launch_rows<0, EPT>(a, rows, stream);
+  return launch_rows<0, EPT>(a, rows, stream);  // longer rows are streamed
 }
 
 }  // namespace
@@ -517,7 +606,7 @@ int topk_launch(const float* x, int64_t rows, int64_t cols, int64_t ld, const in
   a.K = K;
   a.pad_invalid = pad_invalid;
   a.sort = 1;
-  return K <= 8 * kSortThreads ? launch_items<8>(a, rows, stream) : launch_items<32>(a, rows, stream);
+  return K <= 2 * kSortThreads ? launch_items<2>(a, rows, stream) : launch_items<8>(a, rows, stream);
 }
 
 }  // namespace dsa
