@@ -130,7 +130,7 @@ class Layer:
                 events[i][1].record()
 
 
-def cpu_baseline(S1: int, S2: int, budget_rows: int = 32, mla_tokens: int = 96) -> dict:
+def cpu_baseline(S1: int, S2: int, budget_rows: int = 2048, mla_tokens: int = 4096) -> dict:
     """Time the CPU oracle on a bounded sample of the same workload and scale it."""
     import torch
 
@@ -191,6 +191,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_indexer_layer128k.txt"),
                     help="rocprofv3 --pmc summary holding the dominant kernel's HBM bytes per launch")
+    ap.add_argument("--traffic-run", action="store_true",
+                    help="for rocprofv3 --pmc: one 1 GiB device copy (counter calibration), then one "
+                         "layer step; prints no benchmark line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this path "
@@ -200,6 +203,15 @@ def main() -> int:
 
     layer = Layer(args.s1, args.s2, args.dec_batch)
     torch.cuda.synchronize()
+    if args.traffic_run:
+        src = torch.ones((1 << 28,), dtype=torch.float32, device="cuda:0")  # 1 GiB
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        layer.step()
+        torch.cuda.synchronize()
+        print("traffic run: copy of 1073741824 bytes, then one layer step", flush=True)
+        return 0
     for _ in range(args.warmup):
         layer.step()
     torch.cuda.synchronize()
