@@ -120,13 +120,16 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
   const int kbeg = split * p.keys_per_split;
   const int nkeys = max(0, min(p.keys_per_split, p.topk - kbeg));
 
-  // ---- Q^T operand: lane (g, c) holds head c, dims 32ks + 8g .. +8
+  // ---- Q^T operand: lane (g, c) holds head c, dims 64(ks/2) + 16g + 8(ks%2) .. +8,
+  // i.e. 16-byte chunk 8(ks/2) + 2g + ks%2 (the chunk order the K reads use; any
+  // order shared by both operands gives the same dot product)
   dsa::bf16x8 qf[KSTEPS];
   {
-    const uint16_t* qp = p.q + (token * p.H + (head_ok ? head : 0)) * DQK + 8 * g;
+    const uint16_t* qp = p.q + (token * p.H + (head_ok ? head : 0)) * DQK + 16 * g;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
-      dsa::i32x4 v = head_ok ? *reinterpret_cast<const dsa::i32x4*>(qp + 32 * ks) : dsa::i32x4{0, 0, 0, 0};
+      dsa::i32x4 v = head_ok ? *reinterpret_cast<const dsa::i32x4*>(qp + 64 * (ks >> 1) + 8 * (ks & 1))
+                             : dsa::i32x4{0, 0, 0, 0};
       qf[ks] = __builtin_bit_cast(dsa::bf16x8, v);
     }
   }
@@ -213,17 +216,19 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
     if (wave_active) {
       const unsigned char* sb = smem + (step % kStages) * STAGE;
       // S^T = K . Q^T : acc[kt][i] = score(key 16kt + 4g + i, head c); the A
-      // fragment of (kt, ks) is chunk 4ks + g of key 16kt + c.  Reads run
-      // kPre fragments ahead of the MFMAs that consume them.
+      // fragment of (kt, ks) is chunk 8(ks/2) + 2g + ks%2 of key 16kt + c.  Reads
+      // run kPre fragments ahead of the MFMAs that consume them.
       dsa::f32x4 acc[2] = {dsa::f32x4{0.f, 0.f, 0.f, 0.f}, dsa::f32x4{0.f, 0.f, 0.f, 0.f}};
-      // A fragment (kt, ks) = chunk 4ks + g of key 16kt + c: block (kg = 2kt + c/8,
-      // cg = ks/2), in-block key c%8, in-block chunk 4(ks%2) + g  ->  byte offset
-      //   (ks/2) 4096 + kt 2048 + (ks%2 ? kq1 : kq0)
+      // A fragment (kt, ks) = chunk 8(ks/2) + 2g + ks%2 of key 16kt + c: block
+      // (kg = 2kt + c/8, cg = ks/2), in-block key c%8, in-block chunk 2g + ks%2
+      //   ->  byte offset (ks/2) 4096 + kt 2048 + (ks%2 ? kq1 : kq0).
+      // (Group g reading chunks 2g, 2g+1 keeps the 16 rows x 4 groups of one
+      // ds_read_b128 conflict-free, measured; the order 4(ks%2) + g halves the rate.)
       const int qkin = c & 7, qkg1 = (c >> 3) & 1;
       const int qm = qkin ^ qkg1;  // swizzle of this lane's key
-      const uint32_t qbase = (uint32_t)(size_t)(DSA_LDS unsigned char*)(sb + qkg1 * 1024 + qkin * 128 + 16 * (g ^ (qm & 3)));
-      const uint32_t kq0 = qbase + 64 * (qm >> 2);
-      const uint32_t kq1 = qbase + 64 * (1 ^ (qm >> 2));
+      const unsigned char* qrow = sb + qkg1 * 1024 + qkin * 128;
+      const uint32_t kq0 = (uint32_t)(size_t)(DSA_LDS unsigned char*)(qrow + 16 * ((2 * g) ^ qm));
+      const uint32_t kq1 = (uint32_t)(size_t)(DSA_LDS unsigned char*)(qrow + 16 * ((2 * g + 1) ^ qm));
       // fragment f = 2 ks + kt; kPre fragments in flight
       constexpr int kPre = 4;
       dsa::i32x4 kfr[kPre];
