@@ -14,9 +14,11 @@
 // Work decomposition.  One workgroup (8 waves, two per SIMD) handles one token,
 // up to 128 heads (one 16-head MFMA tile per wave; waves past H only help with
 // the gather) and one slice ("split") of the token's index list.  The indexed
-// KV rows (1152 bytes each) are gathered 32 at a time straight into a 4-stage
-// LDS ring with global_load_lds (three steps in flight while one is computed,
-// no staging registers).  A stage is 36 blocks of 1 KB; block (key group kg,
+// KV rows (1152 bytes each) are gathered 32 at a time straight into an LDS ring
+// with global_load_lds (no staging registers): 4 stages (three steps in flight
+// while one is computed) when one workgroup fills a CU, or 2 stages when two
+// workgroups share a CU so that one's prologue and epilogue overlap the other's
+// steps (prefill).  A stage is 36 blocks of 1 KB; block (key group kg,
 // chunk group cg) at (cg * 4 + kg) * 1024 holds keys 8kg .. 8kg+7 x 16-byte chunks
 // 8cg .. 8cg+7, key-major, with chunk c of key k (in-block indices) stored at
 // slot k * 8 + (c ^ k ^ (kg & 1)).  One global_load_lds then fetches whole
@@ -39,7 +41,8 @@ constexpr int kKT = 32;          // keys per step
 constexpr int kDV = 512;         // value dim
 constexpr int kWaves = 8;
 constexpr int kHeadsPerGroup = 16 * kWaves;
-constexpr int kStages = 4;
+constexpr int kStagesWide = 4;  // ring stages when one workgroup fills a CU
+constexpr int kStagesPair = 2;  // ring stages when two workgroups share a CU
 constexpr int kMaxKeysPerSplit = 2048;
 constexpr float kSlack = 8.f;    // log2 headroom of the reference maximum
 
@@ -82,7 +85,7 @@ using dsa::xor32_sum;
 // Source of the gathers for invalid keys: always in bounds, always zero.
 __device__ __align__(16) uint16_t g_zero_row[576];
 
-template <int DQK>
+template <int DQK, int kStages>
 __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
   constexpr int NT = kWaves * 64;
   constexpr int KSTEPS = DQK / 32;          // MFMA k-steps of the score product
@@ -406,10 +409,10 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
   if (d4 == 0 && lse) lse[rh] = den > 0.f ? mx + __logf(den) : -__builtin_inff();
 }
 
-template <int DQK>
-int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
-  const size_t smem = (size_t)kStages * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split;
-  auto fn = sparse_mla_kernel<DQK>;
+template <int DQK, int STAGES>
+int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
+  const size_t smem = (size_t)STAGES * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split;
+  auto fn = sparse_mla_kernel<DQK, STAGES>;
   hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess)
     return dsa::set_error(dsa::kHipError, "sparse_mla: cannot reserve %zu bytes of LDS: %s", smem,
@@ -418,9 +421,20 @@ int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   return dsa::check_launch("dsa_sparse_mla_fwd");
 }
 
+// Two workgroups per CU (2-stage ring, <= 80 KB of LDS each) overlap one's
+// prologue and epilogue with the other's steps: used when there are many
+// workgroups with long index lists (prefill).  Short lists (decode splits) are
+// dominated by gather latency and keep one workgroup per CU with a 4-stage ring.
+template <int DQK>
+int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
+  if (nblocks >= 1024 && p.keys_per_split > 512)
+    return launch_mla_stages<DQK, kStagesPair>(p, nblocks, stream);
+  return launch_mla_stages<DQK, kStagesWide>(p, nblocks, stream);
+}
+
 int choose_splits(int64_t tokens, int nhg, int topk) {
-  // one workgroup per CU fits (LDS); split the index list until the 256 CUs are
-  // covered, keeping >= 256 keys per split
+  // split the index list until the 256 CUs are covered, keeping >= 256 keys per
+  // split (more splits cost more fp32 partials than the extra CUs return)
   int ns = 1;
   while (tokens * nhg * ns < 256 && (topk + 2 * ns - 1) / (2 * ns) >= 256) ns *= 2;
   while ((topk + ns - 1) / ns > kMaxKeysPerSplit) ++ns;
