@@ -130,6 +130,106 @@ class Layer:
                 events[i][1].record()
 
 
+def _time_launches(fn, steps: int, warmup: int = 2) -> float:
+    """Mean microseconds per call of fn() on the current stream (HIP events on that stream)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return 1e3 * sum(a.elapsed_time(b) for a, b in evs) / steps
+
+
+def target_configs(L, steps: int) -> dict:
+    """The single-kernel north-star shapes beside the layer step: sparse-MLA decode
+    (B=64, 64K paged context) and prefill (Sq=Skv=16384), and indexer + top-k at
+    32K (B=1, 4096 x 32768).  Seeded inputs generated on the GPU, resident in HBM."""
+    import torch
+
+    from dsa import inputs
+
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream(dev).cuda_stream
+    res = {}
+
+    def chk(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: {L.dsa_last_error().decode()}")
+
+    # config 3: decode, B=64, 64K context in 64-token pages, top-2048
+    d = inputs.mla_decode(device=dev)
+    B = d["q"].shape[0]
+    out = torch.empty((B, 1, H, DV), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, 1, H), dtype=torch.float32, device=dev)
+    wsb = L.dsa_sparse_mla_workspace_bytes(B, 1, H, TOPK, 0)
+    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+    bt = d["block_table"]
+
+    def dec():
+        chk(L.dsa_sparse_mla_fwd(d["q"].data_ptr(), d["kv"].data_ptr(), d["indices"].data_ptr(), bt.data_ptr(),
+                                 d["seq_len_kv"].data_ptr(), None, None, B, 1, H, DQK, DV, d["kv"].shape[0] * 64,
+                                 64, bt.shape[1], TOPK, DQK ** -0.5, 0, 0, out.data_ptr(), lse.data_ptr(),
+                                 ws.data_ptr(), ws.numel(), st), "decode")
+
+    us = _time_launches(dec, steps)
+    dec_bytes = B * TOPK * (DQK * 2) + B * H * DQK * 2 + B * TOPK * 4 + bt.numel() * 4 + B * H * (DV * 2 + 4)
+    res["decode_b64_64k"] = {"us": round(us, 2), "gbs": round(dec_bytes / us / 1e3, 1),
+                             "frac_of_hbm": round(dec_bytes / us / 1e3 / PEAK_HBM_GBS, 4),
+                             "algorithmic_bytes": dec_bytes}
+    del d, out, lse, ws, bt
+    torch.cuda.empty_cache()
+
+    # config 4: prefill, Sq = Skv = 16384, causal index ranges, top-2048
+    p = inputs.mla_prefill(B=1, S=16384, Skv=16384, H=H, topk=TOPK, seed=4, q_start=0, device=dev)
+    S = p["q"].shape[1]
+    out = torch.empty((1, S, H, DV), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((1, S, H), dtype=torch.float32, device=dev)
+    qs = torch.zeros((1,), dtype=torch.int32, device=dev)
+
+    def pre():
+        chk(L.dsa_sparse_mla_fwd(p["q"].data_ptr(), p["kv"].data_ptr(), p["indices"].data_ptr(), None, None,
+                                 qs.data_ptr(), None, 1, S, H, DQK, DV, S, 0, 0, TOPK, DQK ** -0.5, 1, 1,
+                                 out.data_ptr(), lse.data_ptr(), None, 0, st), "prefill")
+
+    us = _time_launches(pre, max(2, steps // 2))
+    fl = mla_flops(S)
+    res["prefill_16k"] = {"us": round(us, 1), "tflops": round(fl / us / 1e6, 1),
+                          "frac_of_bf16_peak": round(fl / us / 1e6 / PEAK_BF16_TFLOPS, 4)}
+    del p, out, lse
+    torch.cuda.empty_cache()
+
+    # config 2: indexer + top-k, 4096 x 32768
+    S1, S2 = 4096, 32768
+    ix = inputs.indexer_fp8(B=1, S1=S1, S2=S2, seed=2, device=dev)
+    logits = torch.empty((S1, S2), dtype=torch.float32, device=dev)
+    rl = torch.empty((S1,), dtype=torch.int32, device=dev)
+    idx = torch.empty((S1, TOPK), dtype=torch.int32, device=dev)
+
+    def ind():
+        chk(L.dsa_indexer_logits_fp8(ix["q"].data_ptr(), ix["k"].data_ptr(), ix["key_scale"].data_ptr(),
+                                     ix["w"].data_ptr(), None, None, 1, S1, S2, IDX_HEADS, IDX_DIM, 3,
+                                     logits.data_ptr(), S2, rl.data_ptr(), st), "indexer32k")
+
+    def tk():
+        chk(L.dsa_topk_f32(logits.data_ptr(), S1, S2, S2, rl.data_ptr(), TOPK, 1, idx.data_ptr(), None, st),
+            "topk32k")
+
+    ui = _time_launches(ind, steps)
+    ut = _time_launches(tk, steps)
+    fi = indexer_flops_causal(S1, S2)
+    tb = 4.0 * sum(S2 - S1 + t + 1 for t in range(S1)) + 4.0 * S1 * TOPK
+    res["indexer_topk_32k"] = {"indexer_us": round(ui, 1), "topk_us": round(ut, 1),
+                               "indexer_frac_of_fp8_peak": round(fi / ui / 1e6 / PEAK_FP8_TFLOPS, 4),
+                               "topk_frac_of_hbm": round(tb / ut / 1e3 / PEAK_HBM_GBS, 4)}
+    return res
+
+
 def cpu_baseline(S1: int, S2: int, budget_rows: int = 2048, mla_tokens: int = 4096) -> dict:
     """Time the CPU oracle on a bounded sample of the same workload and scale it."""
     import torch
@@ -189,6 +289,8 @@ def main() -> int:
     ap.add_argument("--s2", type=int, default=131072)
     ap.add_argument("--dec-batch", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-targets", action="store_true",
+                    help="skip the single-kernel decode / prefill / 32K indexer timings")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_indexer_layer128k.txt"),
                     help="rocprofv3 --pmc summary holding the dominant kernel's HBM bytes per launch")
     ap.add_argument("--traffic-run", action="store_true",
@@ -280,6 +382,11 @@ def main() -> int:
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
                      "frac": round(ach / peak, 4), "traffic": traffic},
     }
+    if not args.no_targets:
+        lib_handle = layer.L
+        del layer
+        torch.cuda.empty_cache()
+        res["target_configs"] = target_configs(lib_handle, args.steps)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(S1, S2)
     print(json.dumps(res))
