@@ -39,6 +39,22 @@ def test_streamed_long_rows(gpu):
     _assert_exact(*_run(x, 2048, gpu))
 
 
+def test_streamed_ties_and_specials(gpu):
+    # long rows through the sampled-threshold path where the candidate group holds
+    # tie groups larger than a bucket (ordered by the bitonic fallback), NaN, +inf
+    # groups and values straddling zero (value-linear buckets)
+    g = torch.Generator().manual_seed(5)
+    x = torch.round(torch.randn((5, 131072), generator=g) * 4) / 4
+    x[1, ::7] = float("nan")
+    x[2, :1000] = float("inf")
+    x[3] = torch.randn(131072, generator=g) * 1e-30
+    x[4] = torch.randn(131072, generator=g) - 2.1  # the K-th value sits near zero
+    _assert_exact(*_run(x, 2048, gpu))
+    y = torch.round(torch.randn((4, 32768), generator=g) * 8) / 8
+    y[1] = torch.randn(32768, generator=g) + 0.01 * torch.arange(32768) % 3
+    _assert_exact(*_run(y, 2048, gpu))
+
+
 def test_known_answer_arange(gpu):
     # test_topk / test_sort (test_tilelang_ascend_language_elementwise.py:4218-4248, 4059-4086)
     x = torch.arange(0, 51, dtype=torch.float32).reshape(1, 51)

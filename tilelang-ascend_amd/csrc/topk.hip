@@ -1,4 +1,5 @@
-// Row-wise top-k over fp32 scores for gfx950: exact radix select + register sort.
+// Row-wise top-k over fp32 scores for gfx950: sampled threshold, one streaming
+// pass, bucket ordering.
 //
 // Contract (the lightning indexer golden, examples/deepseek_v4/lightning_indexer.py:316-325):
 //   out[r, :] = argsort(-x[r, :L_r], stable=True)[:K]  (descending value, ties to
@@ -10,21 +11,26 @@
 // where ordered() maps fp32 onto uint32 monotonically (-0.0 folded onto +0.0 so
 // they tie, NaN placed below -inf as torch.sort places it last).  All C are
 // distinct and "C larger" == "earlier in the stable descending order", so the
-// top-K set is exactly {C >= C_K} for the K-th largest composite C_K.
+// top-K set is exactly {C >= C_K} for the K-th largest composite C_K and the
+// output order is the descending order of C.
 //
-// Selection.  C_K is found digit by digit (12-bit digits, LDS histograms).
-//  * Rows of up to 16K elements are held in registers and read from HBM once.
+// Selection.
+//  * Rows of up to 16K elements are held in registers and read from HBM once;
+//    longer rows are streamed with double-buffered 16-byte loads.
 //  * Rows of at least 8 K elements: a sample of the row (64-element blocks spread
 //    over it) gives a threshold T whose estimated count above it is ~1.25 K; one
-//    pass (over the registers, or a double-buffered vectorised stream for longer
-//    rows) then copies every element >= T into LDS.  If at least K and at most the LDS
-//    capacity landed there, the top K are exactly among them and the remaining
-//    digits are resolved in LDS; otherwise exact histogram passes over the row
-//    take over.
-// Ordering.  The K chosen composites are bitonic-sorted (descending) by all
-// 1024 threads holding 2 (or 8) keys each: strides below that stay in registers,
-// strides up to 64 threads use VALU cross-lane exchanges (DPP, permlane swaps),
-// only the largest strides go through LDS.
+//    pass copies every element >= T into an LDS candidate group.  If at least K
+//    and at most the LDS capacity landed there, the top K are among them.
+//  * Otherwise C_K is found exactly, digit by digit (12-bit digits, LDS
+//    histograms over the row, then over the LDS group once it fits).
+// Ordering (and, for a candidate group, the exact selection at the same time):
+// the group is bucketed by value key (4096 buckets over its key range), one
+// block-wide scan gives each bucket's output offset and the bucket holding
+// position K - 1, and each element's position is its bucket offset plus the
+// number of larger composites in its bucket (<= 256 of them).  A group with a
+// larger bucket where it matters (heavy ties) is ordered by a bitonic sort of the
+// selection instead: 1024 threads holding 2 (or 8) keys each, register, DPP /
+// permlane and LDS exchanges by stride.
 #include "dsa_common.h"
 
 namespace {
@@ -33,9 +39,10 @@ constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kHistBits = 12;
 constexpr int kBins = 1 << kHistBits;
-constexpr int kCandCap = 5888;     // LDS candidate capacity (46 KB; two blocks fit per CU)
+constexpr int kCandCap = 5760;     // LDS candidate capacity (45 KB; with K <= 2048 two blocks fit per CU)
 constexpr int kSortThreads = kThreads;
 constexpr int kSampleBlocks = 128; // 64-element blocks sampled from a long row
+constexpr int kBucketMax = 256;    // largest bucket the bucket ordering ranks directly
 
 __device__ __forceinline__ uint32_t ordered_key(float f) {
   uint32_t u = __float_as_uint(f);
@@ -63,6 +70,9 @@ struct Shared {
   uint32_t res_bucket;
   uint32_t res_above;
   uint32_t res_count;
+  uint32_t res_key;
+  uint32_t wred[2][kWaves];  // per-wave key min / max
+  uint32_t flag;
 };
 
 // Exclusive prefix sum over the 1024 threads of the block.
@@ -228,29 +238,150 @@ __device__ __forceinline__ void sort_desc(uint64_t* buf, uint64_t* xbuf) {
 
 struct TopkArgs {
   const float* x;          // [rows, ld]
-  const int32_t* in_idx;   // [rows, ld] original indices of x's columns, or null (= column)
   const int32_t* row_len;  // [rows] or null
   int32_t* out_idx;        // [rows, K]
   float* out_val;          // [rows, K] or null
   int64_t ld;
-  int32_t cols, K, pad_invalid, sort;
+  int32_t cols, K, pad_invalid;
 };
+
+// Bucket of value key u among the keys [kmin, kmax] of the group being ordered:
+// non-increasing in u (bucket 0 holds the largest values), equal keys share a
+// bucket.  Linear in the value when the group straddles zero, else linear in
+// the key (logarithmic in |value|).
+struct BucketMap {
+  uint32_t kmax;
+  float vmax, scale;
+  bool by_value;
+  __device__ __forceinline__ int operator()(uint32_t u) const {
+    const float f = by_value ? (vmax - key_value(u)) * scale : (float)(kmax - u) * scale;
+    const int b = (int)f;
+    return b < kBins - 1 ? b : kBins - 1;
+  }
+};
+
+// The bucket map of the key range [kmin, kmax] (the map is evaluated on keys
+// inside that range only).
+__device__ __forceinline__ BucketMap make_map(uint32_t kmin, uint32_t kmax) {
+  BucketMap map;
+  map.kmax = kmax;
+  map.vmax = key_value(kmax);
+  // straddling zero: kmin negative (and not NaN: key 0), kmax non-negative
+  map.by_value = kmin != 0u && kmin < 0x80000000u && kmax >= 0x80000000u;
+  if (map.by_value) {
+    const float s = (float)kBins * 0.99999f / (map.vmax - key_value(kmin));
+    map.by_value = s < __builtin_inff() && s > 0.f;  // finite range
+    map.scale = s;
+  }
+  if (!map.by_value) map.scale = (float)kBins / ((float)(kmax - kmin) + 1.0f);
+  return map;
+}
+
+// Block-wide min and max of one key per thread; every thread gets both.  Ends
+// with a barrier.
+__device__ __forceinline__ void block_minmax(uint32_t& kmin, uint32_t& kmax, Shared& sh) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t a = (uint32_t)__shfl_xor((int)kmin, o, 64), b = (uint32_t)__shfl_xor((int)kmax, o, 64);
+    kmin = a < kmin ? a : kmin;
+    kmax = b > kmax ? b : kmax;
+  }
+  if (lane == 0) {
+    sh.wred[0][wid] = kmin;
+    sh.wred[1][wid] = kmax;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const uint32_t a = sh.wred[0][w], b = sh.wred[1][w];
+    kmin = a < kmin ? a : kmin;
+    kmax = b > kmax ? b : kmax;
+  }
+}
+
+// Orders the K largest of src[0, n) (distinct composites, K <= n): bucket
+// counts over the value keys, one block-wide scan, a scatter into dst (which
+// holds K + kBucketMax entries), and the rank of each element inside its bucket
+// by direct comparison; the ordered K are staged in src[0, K) and handed to
+// emit(p, C) for every position p in [0, K), consecutive threads taking
+// consecutive positions.  Returns false (block-uniform, nothing emitted, src
+// intact) when a bucket that reaches position K - 1 holds more than kBucketMax
+// elements.  All threads of the block must call it.
+template <typename Emit>
+__device__ bool bucket_order(uint64_t* src, int n, int K, uint64_t* dst, Shared& sh, Emit&& emit) {
+  const int tid = threadIdx.x;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+  for (int i = tid; i < n; i += kThreads) {
+    const uint32_t k = (uint32_t)(src[i] >> 32);
+    kmin = k < kmin ? k : kmin;
+    kmax = k > kmax ? k : kmax;
+  }
+  if (tid == 0) sh.flag = 0u;
+  clear_hist(sh);
+  block_minmax(kmin, kmax, sh);
+  const BucketMap map = make_map(kmin, kmax);
+
+  for (int i = tid; i < n; i += kThreads) atomicAdd(&sh.hist[map((uint32_t)(src[i] >> 32))], 1u);
+  __syncthreads();
+  // thread t owns buckets 4t .. 4t + 3; bucket b lies at or before the one
+  // holding position K - 1 exactly when its start is <= K - 1
+  const int b0 = 4 * tid;
+  const uint32_t c0 = sh.hist[b0], c1 = sh.hist[b0 + 1], c2 = sh.hist[b0 + 2], c3 = sh.hist[b0 + 3];
+  const uint32_t local = c0 + c1 + c2 + c3;
+  const uint32_t s0 = block_exclusive_scan(local, sh.wsum);
+  const uint32_t s1 = s0 + c0, s2 = s1 + c1, s3 = s2 + c2;
+  sh.hist[b0] = s0;
+  sh.hist[b0 + 1] = s1;
+  sh.hist[b0 + 2] = s2;
+  sh.hist[b0 + 3] = s3;
+  const uint32_t last = (uint32_t)K - 1u;
+  if (s0 <= last && last < s0 + local)
+    sh.res_bucket = (uint32_t)b0 + (last < s1 ? 0u : last < s2 ? 1u : last < s3 ? 2u : 3u);
+  const uint32_t cap = (uint32_t)kBucketMax;
+  if ((s0 <= last && c0 > cap) || (s1 <= last && c1 > cap) || (s2 <= last && c2 > cap) || (s3 <= last && c3 > cap))
+    sh.flag = 1u;
+  __syncthreads();
+  if (sh.flag != 0u) return false;
+  const int bK = (int)sh.res_bucket;
+  for (int i = tid; i < n; i += kThreads) {
+    const uint64_t C = src[i];
+    const int b = map((uint32_t)(C >> 32));
+    if (b <= bK) dst[atomicAdd(&sh.hist[b], 1u)] = C;
+  }
+  __syncthreads();
+  // hist[b] is now the end of bucket b (= the start of bucket b + 1)
+  const int total = (int)sh.hist[bK];
+  for (int i = tid; i < total; i += kThreads) {
+    const uint64_t C = dst[i];
+    const int b = map((uint32_t)(C >> 32));
+    const int lo = b > 0 ? (int)sh.hist[b - 1] : 0, hi = (int)sh.hist[b];
+    int rank = 0;
+    for (int j = lo; j < hi; ++j) rank += dst[j] > C ? 1 : 0;
+    if (lo + rank < K) src[lo + rank] = C;
+  }
+  __syncthreads();
+  for (int p = tid; p < K; p += kThreads) emit(p, src[p]);
+  return true;
+}
 
 // ITEMS > 0: the row (length <= ITEMS * 1024) lives in registers, element
 // e = j * 1024 + tid for j < ITEMS.  ITEMS == 0: the row is streamed.
-// EPT: keys per sorting thread (the sort covers EPT * 256 >= K keys).
+// EPT: keys per thread of the fallback bitonic sort (EPT * 1024 >= K).
 template <int ITEMS, int EPT>
-__global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ITEMS == 0 ? 8 : 1))) void topk_rows_kernel(TopkArgs a) {
   constexpr int P2 = EPT * kSortThreads;
+  constexpr int kSel = P2 + kBucketMax;                                        // sel entries
+  constexpr int kCand = kCandCap > P2 + kBucketMax ? kCandCap : P2 + kBucketMax;  // cand entries
   extern __shared__ __align__(16) unsigned char smem[];
   Shared* const sh = reinterpret_cast<Shared*>(smem);
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem + ((sizeof(Shared) + 15) & ~size_t(15)));
-  uint64_t* cand = sel + P2;  // max(kCandCap, P2) entries; also the sort's exchange area
+  uint64_t* cand = sel + kSel;  // also the bitonic sort's exchange area
 
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
   const int64_t row = blockIdx.x;
   const float* xr = a.x + row * a.ld;
-  const int32_t* ir = a.in_idx ? a.in_idx + row * a.ld : nullptr;
   const int K = a.K;
   int L = a.cols;
   if (a.row_len != nullptr) {
@@ -261,7 +392,15 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
     sh->cnt[0] = 0u;
     sh->cnt[1] = 0u;
   }
-  auto idx_of = [=](int e) -> uint32_t { return ir ? (uint32_t)ir[e] : (uint32_t)e; };
+  int32_t* orow = a.out_idx + row * (int64_t)K;
+  float* vrow = a.out_val ? a.out_val + row * (int64_t)K : nullptr;
+  auto emit = [=](int p, uint64_t C) {
+    const float val = key_value((uint32_t)(C >> 32));
+    int32_t idx = (int32_t)(~(uint32_t)C);
+    if (a.pad_invalid && val <= -1e30f) idx = -1;
+    orow[p] = idx;
+    if (vrow) vrow[p] = val;
+  };
 
   uint32_t keys[ITEMS > 0 ? ITEMS : 1];
   if constexpr (ITEMS > 0) {
@@ -283,7 +422,7 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
       if ((reinterpret_cast<uintptr_t>(xr) & 15) == 0) {
         // U float4 per thread per batch; the next batch's loads are issued
         // before the current batch is processed.
-        constexpr int U = 4;
+        constexpr int U = 2;
         constexpr int kStep = 4 * kThreads * U;
         const int L4 = L & ~3;
         auto load = [=](dsa::f32x4 (&v)[U], int base) {
@@ -319,77 +458,42 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
     }
   };
 
-  // visit the row in batches: g(k, e, ok) with arrays of the batch's keys, element
-  // indices and validity.  All lanes of a wave take part in every call (the loop
-  // bounds are wave-uniform), so g may use ballots.
-  auto for_each_batch = [=](auto&& g) {
-    if constexpr (ITEMS > 0) {
-      uint32_t kk[ITEMS];
-      int ee[ITEMS];
-      bool ok[ITEMS];
+  // Wave-aggregated append of the lanes whose hit[j] is set: slots from
+  // ballots, one LDS atomic per wave and call.  All lanes of the wave call it.
+  auto append = [=](auto&& hit, auto&& payload, auto NJ) {
+    constexpr int N = decltype(NJ)::value;
+    uint64_t m[N];
+    uint32_t tot = 0;
 #pragma unroll
-      for (int j = 0; j < ITEMS; ++j) {
-        ee[j] = j * kThreads + tid;
-        ok[j] = ee[j] < L;
-        kk[j] = keys[j];
-      }
-      g(kk, ee, ok);
-    } else {
-      constexpr int U = 4;
-      constexpr int kStep = 4 * kThreads * U;
-      const bool vec = (reinterpret_cast<uintptr_t>(xr) & 15) == 0;
-      const int L4 = vec ? (L & ~3) : 0;
-      const int wbase = 4 * (tid & ~63);  // this wave's first element in a batch
-      auto load = [=](dsa::f32x4 (&v)[U], int base) {
+    for (int j = 0; j < N; ++j) {
+      m[j] = __ballot(hit(j));
+      tot += (uint32_t)__popcll(m[j]);
+    }
+    if (tot != 0) {
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(&sh->cnt[1], tot);
+      base = __builtin_amdgcn_readfirstlane(base);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int e = base + 4 * kThreads * u;
-          v[u] = e < L4 ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e))
-                        : dsa::f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < N; ++j) {
+        if (m[j] != 0) {
+          const uint32_t slot =
+              base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m[j] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m[j], 0u));
+          if (hit(j) && slot < (uint32_t)kCandCap) cand[slot] = payload(j);
+          base += (uint32_t)__popcll(m[j]);
         }
-      };
-      auto consume = [=](const dsa::f32x4 (&v)[U], int base) {
-        uint32_t kk[4 * U];
-        int ee[4 * U];
-        bool ok[4 * U];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int e = base + 4 * kThreads * u + q;
-            ee[4 * u + q] = e;
-            ok[4 * u + q] = e < L4;
-            kk[4 * u + q] = ordered_key(v[u][q]);
-          }
-        g(kk, ee, ok);
-      };
-      dsa::f32x4 va[U], vb[U];
-      if (wbase < L4) load(va, 4 * tid);
-      for (int b0 = 0; wbase + b0 < L4; b0 += 2 * kStep) {
-        const bool more1 = wbase + b0 + kStep < L4, more2 = wbase + b0 + 2 * kStep < L4;
-        if (more1) load(vb, 4 * tid + b0 + kStep);
-        consume(va, 4 * tid + b0);
-        if (more2) load(va, 4 * tid + b0 + 2 * kStep);
-        if (more1) consume(vb, 4 * tid + b0 + kStep);
-      }
-      // the scalar tail (and unaligned rows): one element per lane per call
-      for (int e0 = L4; e0 < L; e0 += kThreads) {
-        const int e = e0 + tid;
-        uint32_t kk[1] = {e < L ? ordered_key(xr[e]) : 0u};
-        int ee[1] = {e};
-        bool ok[1] = {e < L};
-        g(kk, ee, ok);
       }
     }
   };
 
-  int nsel_final;
+  int nsel = K;          // selected entries (min(K, L))
+  bool ordered = false;  // the output is written
   if (L <= K) {
     // Everything is selected.
     __syncthreads();
-    for_each([=](uint32_t key, int e) { sel[e] = composite(key, idx_of(e)); });
-    nsel_final = L;
+    for_each([=](uint32_t key, int e) { sel[e] = composite(key, (uint32_t)e); });
+    nsel = L;
     __syncthreads();
+    if (L > 0) ordered = bucket_order(sel, L, L, cand, *sh, emit);
   } else {
     uint32_t need = (uint32_t)K;
     uint64_t P = 0;
@@ -400,94 +504,214 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
 
     {
       // ---- sampled threshold, then one pass collecting everything above it ----
-      uint32_t* samp = reinterpret_cast<uint32_t*>(cand);  // up to kSampleBlocks * 64 keys
-      // nb blocks of 64, at most a quarter of the row
-      const int nb = (L / 256) < kSampleBlocks ? (L / 256) : kSampleBlocks;
+      // nb blocks of 64 spread over the row, sized for ~164 sample elements above
+      // the threshold (clamped to [16, 128] blocks and at most a quarter of the row)
+      const int64_t want = (164ll * L + 64ll * (K + K / 4 + 64) - 1) / (64ll * (K + K / 4 + 64));
+      int nb = want < 16 ? 16 : (want > kSampleBlocks ? kSampleBlocks : (int)want);
+      if (nb > L / 256) nb = L / 256;
       const int ns = nb * 64;
       if (L >= 8 * K && nb >= 16) {
-        for (int i = tid; i < ns; i += kThreads) {
+        constexpr int kPer = kSampleBlocks * 64 / kThreads;
+        uint32_t sv[kPer];
+        uint32_t smin = 0xffffffffu, smax = 0u;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+          const int i = tid + u * kThreads;
           const int blk = i >> 6;
           const int start = (int)(((int64_t)blk * L / nb) & ~63);
-          samp[i] = ordered_key(xr[start + (i & 63)]);
+          sv[u] = i < ns ? ordered_key(xr[start + (i & 63)]) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+          if (tid + u * kThreads < ns) {
+            smin = sv[u] < smin ? sv[u] : smin;
+            smax = sv[u] > smax ? sv[u] : smax;
+          }
         }
         // rank of the threshold inside the sample: ~1.25 K + 64 expected above it
         const uint32_t r = (uint32_t)(((int64_t)(K + K / 4 + 64) * ns + L - 1) / L);
+        // histogram of the sample over buckets spread evenly across its own key
+        // range (bin kBins - 1 - bucket: larger values in higher bins)
         clear_hist(*sh);
-        __syncthreads();
-        for (int i = tid; i < ns; i += kThreads) atomicAdd(&sh->hist[samp[i] >> 20], 1u);
+        block_minmax(smin, smax, *sh);
+        const BucketMap smap = make_map(smin, smax);
+#pragma unroll
+        for (int u = 0; u < kPer; ++u)
+          if (tid + u * kThreads < ns) atomicAdd(&sh->hist[kBins - 1 - smap(sv[u])], 1u);
         __syncthreads();
         find_bucket(*sh, r);
-        const uint32_t b1 = sh->res_bucket, r2 = r - sh->res_above;
-        __syncthreads();
-        clear_hist(*sh);
-        __syncthreads();
-        for (int i = tid; i < ns; i += kThreads)
-          if ((samp[i] >> 20) == b1) atomicAdd(&sh->hist[(samp[i] >> 8) & 0xfffu], 1u);
-        __syncthreads();
-        find_bucket(*sh, r2);
-        const uint32_t T = (b1 << 20) | (sh->res_bucket << 8);
-        __syncthreads();
-        // wave-aggregated append: slots from ballots, one LDS atomic per wave and batch
-        const int lane = tid & 63;
-        for_each_batch([=](const auto& kk, const auto& ee, const auto& ok) {
-          constexpr int NB = sizeof(kk) / sizeof(kk[0]);
-          uint32_t off[NB];
-          uint32_t tot = 0;
-#pragma unroll
-          for (int j = 0; j < NB; ++j) {
-            const uint64_t m = __ballot(ok[j] && kk[j] >= T);
-            off[j] = tot + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-            tot += (uint32_t)__popcll(m);
+        const int mstar = kBins - 1 - (int)sh->res_bucket;
+        // T = the smallest key whose bucket is <= mstar (the map is non-increasing
+        // in the key and maps smax to 0): a 64-way search by wave 0
+        if (tid < 64) {
+          uint32_t lo = smin, hi = smax;
+          while (lo < hi) {
+            const uint32_t step = (hi - lo) / 63u + 1u;  // lane 63 reaches hi
+            const uint64_t p64 = (uint64_t)lo + (uint64_t)step * (uint32_t)lane;
+            const uint32_t p = p64 < hi ? (uint32_t)p64 : hi;
+            const uint64_t okm = __ballot(smap(p) <= mstar);
+            const int f = __builtin_ctzll(okm);  // lane 63 probes hi at the latest
+            const uint32_t pf = (uint32_t)__builtin_amdgcn_readlane((int)p, f);
+            lo = f > 0 ? (uint32_t)__builtin_amdgcn_readlane((int)p, f - 1) + 1u : lo;
+            hi = pf;
           }
-          if (tot != 0) {
-            uint32_t base = 0;
-            if (lane == 0) base = atomicAdd(&sh->cnt[1], tot);
-            base = __builtin_amdgcn_readfirstlane(base);
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-              const uint32_t slot = base + off[j];
-              if (ok[j] && kk[j] >= T && slot < (uint32_t)kCandCap) cand[slot] = composite(kk[j], idx_of(ee[j]));
-            }
-          }
-        });
-        __syncthreads();
-        const uint32_t nc = sh->cnt[1];
-        __syncthreads();
-        if (nc >= (uint32_t)K && nc <= (uint32_t)kCandCap) {
-          // the top K all lie among the candidates: the group is all of them
-          have_cand = true;
-        } else if (tid == 0) {
-          sh->cnt[1] = 0u;  // fall back to the exact passes below
+          if (lane == 0) sh->res_key = lo;
         }
         __syncthreads();
+        uint32_t T = sh->res_key;
+        // keys in (0, key(-inf)) do not occur: lift T onto -inf's key so that the
+        // float compare below sees a real threshold; T == 0 (NaN included) is
+        // left to the exact passes
+        if (T != 0u && T < 0x007fffffu) T = 0x007fffffu;
+        if (T != 0u) {
+          if constexpr (ITEMS > 0) {
+            append([&](int j) { return j * kThreads + tid < L && keys[j] >= T; },
+                   [&](int j) { return composite(keys[j], (uint32_t)(j * kThreads + tid)); }, IntC<ITEMS>{});
+          } else {
+            // streamed: compare the raw floats with T's value (for non-NaN x,
+            // x >= value(T) <=> ordered(x) >= T) and store (bits, index); the
+            // composites are formed afterwards, for the candidates only
+            const float Tf = key_value(T);
+            constexpr int kStep = 8 * kThreads;  // two float4 per thread per batch
+            const bool vec = (reinterpret_cast<uintptr_t>(xr) & 15) == 0;
+            const int L4 = vec ? (L & ~3) : 0;
+            const int wbase = 4 * (tid & ~63);  // this wave's first element in a batch
+            auto load = [=](dsa::f32x4& v0, dsa::f32x4& v1, int e) {
+              const dsa::f32x4 z = {0.f, 0.f, 0.f, 0.f};
+              v0 = e < L4 ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e)) : z;
+              v1 = e + 4 * kThreads < L4
+                       ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e + 4 * kThreads))
+                       : z;
+            };
+            auto consume = [&](const dsa::f32x4& v0, const dsa::f32x4& v1, int e) {
+              const bool ok0 = e < L4, ok1 = e + 4 * kThreads < L4;
+              const bool h[8] = {ok0 && v0[0] >= Tf, ok0 && v0[1] >= Tf, ok0 && v0[2] >= Tf, ok0 && v0[3] >= Tf,
+                                 ok1 && v1[0] >= Tf, ok1 && v1[1] >= Tf, ok1 && v1[2] >= Tf, ok1 && v1[3] >= Tf};
+              uint64_t m[8];
+              uint32_t tot = 0;
+#pragma unroll
+              for (int j = 0; j < 8; ++j) {
+                m[j] = __ballot(h[j]);
+                tot += (uint32_t)__popcll(m[j]);
+              }
+              if (tot != 0) {
+                uint32_t base = 0;
+                if (lane == 0) base = atomicAdd(&sh->cnt[1], tot);
+                base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                  if (m[j] != 0) {
+                    const uint32_t slot = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m[j] >> 32),
+                                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)m[j], 0u));
+                    const float x = j < 4 ? v0[j & 3] : v1[j & 3];
+                    const int ej = e + (j < 4 ? 0 : 4 * kThreads) + (j & 3);
+                    if (h[j] && slot < (uint32_t)kCandCap)
+                      cand[slot] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)ej;
+                    base += (uint32_t)__popcll(m[j]);
+                  }
+                }
+              }
+            };
+            dsa::f32x4 a0, a1, b0v, b1v;
+            if (wbase < L4) load(a0, a1, 4 * tid);
+            for (int c0 = 0; wbase + c0 < L4; c0 += 2 * kStep) {
+              const bool more1 = wbase + c0 + kStep < L4, more2 = wbase + c0 + 2 * kStep < L4;
+              if (more1) load(b0v, b1v, 4 * tid + c0 + kStep);
+              consume(a0, a1, 4 * tid + c0);
+              if (more2) load(a0, a1, 4 * tid + c0 + 2 * kStep);
+              if (more1) consume(b0v, b1v, 4 * tid + c0 + kStep);
+            }
+            // the scalar tail (and unaligned rows): one element per lane per call
+            for (int e0 = L4; e0 < L; e0 += kThreads) {
+              const int e = e0 + tid;
+              const float x = e < L ? xr[e] : 0.f;
+              append([&](int) { return e < L && x >= Tf; },
+                     [&](int) { return ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)e; }, IntC<1>{});
+            }
+          }
+          __syncthreads();
+          const uint32_t nc = sh->cnt[1];
+          have_cand = nc >= (uint32_t)K && nc <= (uint32_t)kCandCap;
+          if constexpr (ITEMS == 0) {
+            if (have_cand) {
+              for (int i = tid; i < (int)nc; i += kThreads) {
+                const uint64_t raw = cand[i];
+                cand[i] = composite(ordered_key(__uint_as_float((uint32_t)(raw >> 32))), (uint32_t)raw);
+              }
+            }
+          }
+          __syncthreads();
+          if (!have_cand && tid == 0) sh->cnt[1] = 0u;  // fall back to the exact passes below
+          if (have_cand) ordered = bucket_order(cand, (int)nc, K, sel, *sh, emit);
+          __syncthreads();
+        }
       }
     }
 
-    if (!have_cand) {
-      // ---- exact pass 1 over the row: top 12 bits of the value key ----
-      clear_hist(*sh);
-      __syncthreads();
-      for_each([=](uint32_t key, int) { atomicAdd(&sh->hist[key >> 20], 1u); });
-      __syncthreads();
-      find_bucket(*sh, need);
-      P = sh->res_bucket;
-      s = 64 - kHistBits;
-      need -= sh->res_above;
-      cnt = sh->res_count;
-      done = (cnt == need);
-      __syncthreads();
+    if (!ordered) {
+      if (!have_cand) {
+        // ---- exact pass 1 over the row: top 12 bits of the value key ----
+        clear_hist(*sh);
+        __syncthreads();
+        for_each([=](uint32_t key, int) { atomicAdd(&sh->hist[key >> 20], 1u); });
+        __syncthreads();
+        find_bucket(*sh, need);
+        P = sh->res_bucket;
+        s = 64 - kHistBits;
+        need -= sh->res_above;
+        cnt = sh->res_count;
+        done = (cnt == need);
+        __syncthreads();
 
-      // ---- further passes over the row while the group is too large for LDS ----
-      while (!done && s > 0 && cnt > (uint32_t)kCandCap) {
+        // ---- further passes over the row while the group is too large for LDS ----
+        while (!done && s > 0 && cnt > (uint32_t)kCandCap) {
+          const int w = s < kHistBits ? s : kHistBits;
+          const int s2 = s - w;
+          const uint64_t dmask = (1ull << w) - 1ull;
+          clear_hist(*sh);
+          __syncthreads();
+          for_each([=](uint32_t key, int e) {
+            const uint64_t C = composite(key, (uint32_t)e);
+            if (high_bits(C, s) == P) atomicAdd(&sh->hist[(uint32_t)((C >> s2) & dmask)], 1u);
+          });
+          __syncthreads();
+          find_bucket(*sh, need);
+          P = (P << w) | sh->res_bucket;
+          s = s2;
+          need -= sh->res_above;
+          cnt = sh->res_count;
+          done = (cnt == need);
+          __syncthreads();
+        }
+
+        // ---- collect: strictly-above elements are selected; the group goes to LDS ----
+        for_each([=](uint32_t key, int e) {
+          const uint64_t C = composite(key, (uint32_t)e);
+          const uint64_t hi = high_bits(C, s);
+          const bool to_sel = hi > P || (done && hi == P);
+          if (to_sel || hi == P) {
+            const int which = to_sel ? 0 : 1;
+            const uint32_t slot = atomicAdd(&sh->cnt[which], 1u);
+            if (to_sel) sel[slot] = C;
+            else cand[slot] = C;
+          }
+        });
+        __syncthreads();
+      }
+      const int ncand = (int)sh->cnt[1];
+
+      // ---- resolve the remaining digits inside the LDS candidate group ----
+      // (composites are distinct, so the group shrinks to the single C_K by s == 0)
+      while (!done && s > 0) {
         const int w = s < kHistBits ? s : kHistBits;
         const int s2 = s - w;
         const uint64_t dmask = (1ull << w) - 1ull;
         clear_hist(*sh);
         __syncthreads();
-        for_each([=](uint32_t key, int e) {
-          const uint64_t C = composite(key, idx_of(e));
+        for (int i = tid; i < ncand; i += kThreads) {
+          const uint64_t C = cand[i];
           if (high_bits(C, s) == P) atomicAdd(&sh->hist[(uint32_t)((C >> s2) & dmask)], 1u);
-        });
+        }
         __syncthreads();
         find_bucket(*sh, need);
         P = (P << w) | sh->res_bucket;
@@ -497,81 +721,37 @@ __global__ __launch_bounds__(kThreads) void topk_rows_kernel(TopkArgs a) {
         done = (cnt == need);
         __syncthreads();
       }
-
-      // ---- collect: strictly-above elements are selected; the group goes to LDS ----
-      for_each([=](uint32_t key, int e) {
-        const uint64_t C = composite(key, idx_of(e));
-        const uint64_t hi = high_bits(C, s);
-        // strictly above -> sel (slot in [0, P2)), the group -> cand (slot P2 + i):
-        // one LDS pool indexed arithmetically
-        const bool to_sel = hi > P || (done && hi == P);
-        if (to_sel || hi == P) {
-          const int which = to_sel ? 0 : 1;
-          const uint32_t slot = atomicAdd(&sh->cnt[which], 1u);
-          sel[slot + (to_sel ? 0u : (uint32_t)P2)] = C;
-        }
-      });
-      __syncthreads();
-    }
-    const int ncand = (int)sh->cnt[1];
-
-    // ---- resolve the remaining digits inside the LDS candidate group ----
-    // (composites are distinct, so the group shrinks to the single C_K by s == 0)
-    while (!done && s > 0) {
-      const int w = s < kHistBits ? s : kHistBits;
-      const int s2 = s - w;
-      const uint64_t dmask = (1ull << w) - 1ull;
-      clear_hist(*sh);
-      __syncthreads();
       for (int i = tid; i < ncand; i += kThreads) {
         const uint64_t C = cand[i];
-        if (high_bits(C, s) == P) atomicAdd(&sh->hist[(uint32_t)((C >> s2) & dmask)], 1u);
+        if (high_bits(C, s) >= P) sel[atomicAdd(&sh->cnt[0], 1u)] = C;
       }
       __syncthreads();
-      find_bucket(*sh, need);
-      P = (P << w) | sh->res_bucket;
-      s = s2;
-      need -= sh->res_above;
-      cnt = sh->res_count;
-      done = (cnt == need);
-      __syncthreads();
+      // sel[0, K) holds the selection; order it by buckets unless the candidate
+      // group already failed to (then the bitonic sort below takes it)
+      if (!have_cand) ordered = bucket_order(sel, K, K, cand, *sh, emit);
     }
-    for (int i = tid; i < ncand; i += kThreads) {
-      const uint64_t C = cand[i];
-      if (high_bits(C, s) >= P) sel[atomicAdd(&sh->cnt[0], 1u)] = C;
-    }
-    __syncthreads();
-    nsel_final = K;
   }
 
-  if (a.sort) {
-    for (int i = nsel_final + tid; i < P2; i += kThreads) sel[i] = 0ull;  // pad: smallest composite
+  if (!ordered && nsel > 0) {
+    // fallback ordering: bitonic sort of the whole selection
+    for (int i = nsel + tid; i < P2; i += kThreads) sel[i] = 0ull;  // pad: smallest composite
     __syncthreads();
-    constexpr bool kDouble = (kCandCap > P2 ? kCandCap : P2) >= 2 * P2;
+    constexpr bool kDouble = kCand >= 2 * P2;
     sort_desc<EPT, kDouble>(sel, cand);
+    for (int p = tid; p < nsel; p += kThreads) emit(p, sel[p]);
   }
-
-  int32_t* orow = a.out_idx + row * (int64_t)K;
-  float* vrow = a.out_val ? a.out_val + row * (int64_t)K : nullptr;
-  for (int p = tid; p < K; p += kThreads) {
-    int32_t idx = -1;
-    float val = -__builtin_inff();
-    if (p < nsel_final) {
-      const uint64_t C = sel[p];
-      val = key_value((uint32_t)(C >> 32));
-      idx = (int32_t)(~(uint32_t)C);
-      if (a.pad_invalid && val <= -1e30f) idx = -1;
-    }
-    orow[p] = idx;
-    if (vrow) vrow[p] = val;
+  for (int p = nsel + tid; p < K; p += kThreads) {
+    orow[p] = -1;
+    if (vrow) vrow[p] = -__builtin_inff();
   }
 }
 
 template <int ITEMS, int EPT>
 int launch_rows(const TopkArgs& a, int64_t rows, hipStream_t stream) {
   constexpr int P2 = EPT * kSortThreads;
-  const size_t smem = ((sizeof(Shared) + 15) & ~size_t(15)) +
-                      sizeof(uint64_t) * (size_t)(P2 + (kCandCap > P2 ? kCandCap : P2));
+  constexpr int kSel = P2 + kBucketMax;
+  constexpr int kCand = kCandCap > P2 + kBucketMax ? kCandCap : P2 + kBucketMax;
+  const size_t smem = ((sizeof(Shared) + 15) & ~size_t(15)) + sizeof(uint64_t) * (size_t)(kSel + kCand);
   auto fn = topk_rows_kernel<ITEMS, EPT>;
   (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   hipLaunchKernelGGL(fn, dim3((unsigned)rows), dim3(kThreads), smem, stream, a);
@@ -597,7 +777,6 @@ int topk_launch(const float* x, int64_t rows, int64_t cols, int64_t ld, const in
   if (rows == 0 || K == 0) return kOk;
   TopkArgs a;
   a.x = x;
-  a.in_idx = nullptr;
   a.row_len = row_len;
   a.out_idx = out_idx;
   a.out_val = out_val;
@@ -605,7 +784,6 @@ int topk_launch(const float* x, int64_t rows, int64_t cols, int64_t ld, const in
   a.cols = (int32_t)cols;
   a.K = K;
   a.pad_invalid = pad_invalid;
-  a.sort = 1;
   return K <= 2 * kSortThreads ? launch_items<2>(a, rows, stream) : launch_items<8>(a, rows, stream);
 }
 
