@@ -98,7 +98,8 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
   uint32_t pre = 0;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) pre += w < wid ? wsum[w] : 0u;  // independent loads
-  __syncthreads();
+  // (wsum is rewritten only by the next scan, and every caller passes another
+  // barrier before that)
   return pre + x - v;
 }
 
@@ -317,18 +318,32 @@ __device__ __forceinline__ void block_minmax(uint32_t& kmin, uint32_t& kmax, Sha
 // consecutive positions.  Returns false (block-uniform, nothing emitted, src
 // intact) when a bucket that reaches position K - 1 holds more than kBucketMax
 // elements.  All threads of the block must call it.
+//
+// With known_range the caller has cleared sh.hist, set sh.flag = 0, stored the
+// per-wave maxima of the keys in sh.wred[1] and passed a barrier; kmin is then a
+// lower bound of the keys (the sampled threshold), which only widens the map.
 template <typename Emit>
-__device__ bool bucket_order(uint64_t* src, int n, int K, uint64_t* dst, Shared& sh, Emit&& emit) {
+__device__ bool bucket_order(uint64_t* src, int n, int K, uint64_t* dst, Shared& sh, Emit&& emit,
+                             bool known_range = false, uint32_t kmin_bound = 0u) {
   const int tid = threadIdx.x;
   uint32_t kmin = 0xffffffffu, kmax = 0u;
-  for (int i = tid; i < n; i += kThreads) {
-    const uint32_t k = (uint32_t)(src[i] >> 32);
-    kmin = k < kmin ? k : kmin;
-    kmax = k > kmax ? k : kmax;
+  if (known_range) {
+    kmin = kmin_bound;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const uint32_t b = sh.wred[1][w];
+      kmax = b > kmax ? b : kmax;
+    }
+  } else {
+    for (int i = tid; i < n; i += kThreads) {
+      const uint32_t k = (uint32_t)(src[i] >> 32);
+      kmin = k < kmin ? k : kmin;
+      kmax = k > kmax ? k : kmax;
+    }
+    if (tid == 0) sh.flag = 0u;
+    clear_hist(sh);
+    block_minmax(kmin, kmax, sh);
   }
-  if (tid == 0) sh.flag = 0u;
-  clear_hist(sh);
-  block_minmax(kmin, kmax, sh);
   const BucketMap map = make_map(kmin, kmax);
 
   for (int i = tid; i < n; i += kThreads) atomicAdd(&sh.hist[map((uint32_t)(src[i] >> 32))], 1u);
@@ -361,13 +376,28 @@ __device__ bool bucket_order(uint64_t* src, int n, int K, uint64_t* dst, Shared&
   __syncthreads();
   // hist[b] is now the end of bucket b (= the start of bucket b + 1)
   const int total = (int)sh.hist[bK];
-  for (int i = tid; i < total; i += kThreads) {
-    const uint64_t C = dst[i];
-    const int b = map((uint32_t)(C >> 32));
-    const int lo = b > 0 ? (int)sh.hist[b - 1] : 0, hi = (int)sh.hist[b];
-    int rank = 0;
-    for (int j = lo; j < hi; ++j) rank += dst[j] > C ? 1 : 0;
-    if (lo + rank < K) src[lo + rank] = C;
+  // three elements per thread at a time so that their LDS round trips overlap
+  for (int i0 = tid; i0 < total; i0 += 3 * kThreads) {
+    uint64_t cv[3];
+    int lo[3], hi[3];
+#pragma unroll
+    for (int u = 0; u < 3; ++u) cv[u] = i0 + u * kThreads < total ? dst[i0 + u * kThreads] : 0ull;
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      const bool ok = i0 + u * kThreads < total;
+      const int b = map((uint32_t)(cv[u] >> 32));
+      lo[u] = ok && b > 0 ? (int)sh.hist[b - 1] : 0;
+      hi[u] = ok ? (int)sh.hist[b] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      int rank = 0;
+      for (int j = lo[u]; j < hi[u]; j += 2) {
+        const uint64_t d0 = dst[j], d1 = j + 1 < hi[u] ? dst[j + 1] : 0ull;
+        rank += (d0 > cv[u] ? 1 : 0) + (d1 > cv[u] ? 1 : 0);
+      }
+      if (i0 + u * kThreads < total && lo[u] + rank < K) src[lo[u] + rank] = cv[u];
+    }
   }
   __syncthreads();
   for (int p = tid; p < K; p += kThreads) emit(p, src[p]);
@@ -643,15 +673,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ITEMS 
           have_cand = nc >= (uint32_t)K && nc <= (uint32_t)kCandCap;
           if constexpr (ITEMS == 0) {
             if (have_cand) {
+              // form the composites, keep the largest key for the bucket map and
+              // clear the histogram it uses (the sampled T bounds the keys below)
+              uint32_t kmx = 0u;
               for (int i = tid; i < (int)nc; i += kThreads) {
                 const uint64_t raw = cand[i];
-                cand[i] = composite(ordered_key(__uint_as_float((uint32_t)(raw >> 32))), (uint32_t)raw);
+                const uint32_t key = ordered_key(__uint_as_float((uint32_t)(raw >> 32)));
+                kmx = key > kmx ? key : kmx;
+                cand[i] = composite(key, (uint32_t)raw);
               }
+              static_for<0, 6>([&](auto D) {
+                constexpr int d = 1 << decltype(D)::value;
+                const uint32_t o = xor_lane<d>(kmx, lane);
+                kmx = o > kmx ? o : kmx;
+              });
+              if (lane == 0) sh->wred[1][tid >> 6] = kmx;
+              if (tid == 0) sh->flag = 0u;
+              clear_hist(*sh);
             }
           }
           __syncthreads();
           if (!have_cand && tid == 0) sh->cnt[1] = 0u;  // fall back to the exact passes below
-          if (have_cand) ordered = bucket_order(cand, (int)nc, K, sel, *sh, emit);
+          if (have_cand) ordered = bucket_order(cand, (int)nc, K, sel, *sh, emit, ITEMS == 0, T);
           __syncthreads();
         }
       }
