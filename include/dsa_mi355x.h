@@ -96,6 +96,49 @@ int dsa_lightning_indexer_fp8(const void* q, const void* k, const float* key_sca
                               void* stream);
 
 /*
+ * Indexer logits for the reference's other key / query layouts
+ * (examples/deepseek_v4/lightning_indexer.py:1256-1302 with its conversions
+ * :48-193), read in place instead of converted:
+ *   seq_q: per-batch query lengths (seq_q_cumulative = 0; rows b * S1 + t, the
+ *          BSND layout) or their prefix sums (= 1; rows seq_q[b-1] + t, the TND
+ *          layout [T, N1, D]); NULL = S1 for every batch.
+ *   seq_k: per-batch key lengths or prefix sums (TND keys [T2, D]); NULL = S2.
+ *   block_table [B, max_blocks] or NULL: keys (and key_scale) live in a page pool
+ *          of pool_rows = blocks * block_size rows (the PA_BSND layout
+ *          [blocks, block_size, 1, D]); key s of batch b is pool row
+ *          block_table[b, s / block_size] * block_size + s % block_size.  Takes
+ *          per-batch key lengths.
+ * S1 / S2 are the largest per-batch query / key lengths (larger lengths are
+ * clipped to them); prefix sums must end at T, so that every query row belongs to
+ * a batch.  logits has one row per query row (B * S1 padded, or T for prefix
+ * sums); row_len likewise, as above.
+ */
+int dsa_indexer_logits_fp8_varlen(const void* q, const void* k, const float* key_scale,
+                                  const float* weights, const int32_t* seq_q, int32_t seq_q_cumulative,
+                                  const int32_t* seq_k, int32_t seq_k_cumulative,
+                                  const int32_t* block_table, int32_t block_size, int32_t max_blocks,
+                                  int64_t pool_rows, int64_t B, int64_t S1, int64_t S2, int32_t N1,
+                                  int32_t D, int32_t sparse_mode, float* logits, int64_t ld,
+                                  int32_t* row_len, void* stream);
+
+/*
+ * Full lightning indexer for those layouts: the logits above, then the top
+ * `sparse_count` of each of the q_rows query rows (q_rows = B * S1 for padded
+ * rows, T for prefix sums).  indices [q_rows, sparse_count] int32 (the TND output
+ * [T, 1, K] of lightning_indexer.py:1365-1368 for prefix sums), values likewise
+ * or NULL.  workspace: dsa_lightning_indexer_varlen_workspace_bytes(q_rows, S2).
+ */
+size_t dsa_lightning_indexer_varlen_workspace_bytes(int64_t q_rows, int64_t S2);
+int dsa_lightning_indexer_fp8_varlen(const void* q, const void* k, const float* key_scale,
+                                     const float* weights, const int32_t* seq_q, int32_t seq_q_cumulative,
+                                     const int32_t* seq_k, int32_t seq_k_cumulative,
+                                     const int32_t* block_table, int32_t block_size, int32_t max_blocks,
+                                     int64_t pool_rows, int64_t B, int64_t S1, int64_t S2, int64_t q_rows,
+                                     int32_t N1, int32_t D, int32_t sparse_count, int32_t sparse_mode,
+                                     int32_t* indices, float* values, void* workspace,
+                                     size_t workspace_bytes, void* stream);
+
+/*
  * Sparse MLA forward: bf16 q [B, S, H, d_qk], one latent KV head, d_v = 512.
  * Replaces the `call` of sparse_attention_fwd
  * (examples/sparse_flash_attention/example_sparse_flash_attn.py:18-243, main(Q, KV,

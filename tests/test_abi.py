@@ -129,9 +129,14 @@ def test_python_layer_rejects_bad_arguments():
         dsa.lightning_indexer(q, k, w, sparse_count=3000)
     with pytest.raises(AssertionError, match="layout"):
         dsa.lightning_indexer(q, k, w, layout_query="XYZ")
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(AssertionError, match="actual_seq_lengths_query"):
         dsa.lightning_indexer(q.view(4, 64, 128), k.view(16, 1, 128), w.view(4, 64),
                               layout_query="TND", layout_key="TND")
+    with pytest.raises(ValueError, match="block_table"):
+        dsa.lightning_indexer(q, k.view(1, 16, 1, 128), w, layout_key="PA_BSND",
+                              actual_seq_lengths_key=torch.tensor([16]))
+    with pytest.raises(ValueError, match="layout_query"):
+        dsa.lightning_indexer(q, k.view(16, 1, 128), w, layout_key="TND")
     with pytest.raises(ValueError, match="dtype"):
         dsa.lightning_indexer(q.float(), k.float(), w)
     bf = torch.bfloat16

@@ -103,3 +103,136 @@ def test_config2_rows_sample(gpu):
         _logit_close(logits[0, t, :L].cpu(), ref)
         ti, _ = stable_topk(logits[0, t, :L].cpu().unsqueeze(0), 2048)
         assert torch.equal(idx[0, t, 0].cpu(), ti[0])
+
+
+def _ragged_fp8(seed, lens_q, lens_k, D=128, H=64):
+    """Ragged fp8 batches with per-key scales (the config-2 recipe per batch)."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((sum(lens_q), H, D), generator=g).to(inputs.FP8)
+    k32 = torch.randn((sum(lens_k), 1, D), generator=g)
+    w = torch.randn((sum(lens_q), H), generator=g) / 8
+    scale = torch.clamp(k32.abs().amax(dim=-1) / 448.0, min=torch.finfo(torch.float32).tiny)  # [T2, 1]
+    k = (k32 / scale.unsqueeze(-1)).to(inputs.FP8)
+    return q, k, w, scale.view(-1)
+
+
+def _cum(lens):
+    return torch.tensor([sum(lens[:i + 1]) for i in range(len(lens))], dtype=torch.int32)
+
+
+@pytest.mark.parametrize("mode", [3, 0])
+def test_tnd_layout(gpu, mode):
+    # TND query and key (varlen rows read in place); reference layout contract
+    # lightning_indexer.py:48-84,111-150,1256-1262,1365-1368
+    lens_q, lens_k, K = [40, 0, 17, 64], [2500, 300, 1024, 4000], 256
+    q, k, w, ks = _ragged_fp8(31 + mode, lens_q, lens_k)
+    print(f"indexer TND lens_q={lens_q} lens_k={lens_k} mode={mode}", flush=True)
+    cq, ck = _cum(lens_q), _cum(lens_k)
+    idx, vals, logits = dsa.lightning_indexer(q.to(gpu), k.to(gpu), w.to(gpu), key_scale=ks.to(gpu),
+                                              actual_seq_lengths_query=cq.to(gpu), actual_seq_lengths_key=ck.to(gpu),
+                                              layout_query="TND", layout_key="TND", sparse_count=K,
+                                              sparse_mode=mode, return_value=True, return_logits=True)
+    torch.cuda.synchronize()
+    assert idx.shape == (sum(lens_q), 1, K) and logits.shape == (sum(lens_q), max(lens_k))
+    ri, rscores, rv = ref_indexer(q, k, w, key_scale=ks, actual_seq_lengths_query=cq, actual_seq_lengths_key=ck,
+                                  layout_query="TND", layout_key="TND", sparse_count=K, sparse_mode=mode)
+    logits, idx = logits.cpu(), idx.cpu()
+    row = 0
+    for b, (aq, ak) in enumerate(zip(lens_q, lens_k)):
+        for t in range(aq):
+            ref = rscores[b, 0, t, :ak]
+            n = int(torch.isfinite(ref).sum())
+            _logit_close(logits[row, :n].unsqueeze(0), ref[:n].unsqueeze(0))
+            ti, _ = stable_topk(logits[row, :n].unsqueeze(0), K)
+            assert torch.equal(idx[row, 0], ti[0]), (b, t)
+            row += 1
+
+
+@pytest.mark.parametrize("block_size", [16, 64, 128])
+def test_paged_keys_match_contiguous(gpu, block_size):
+    # PA_BSND keys through a shuffled block table (lightning_indexer.py:271-292):
+    # identical inputs laid out contiguously give bit-identical logits and indices
+    B, S1, S2, K = 3, 20, 3000, 512
+    inp = inputs.indexer_fp8(B=B, S1=S1, S2=S2, seed=40 + block_size)
+    lens_k = torch.tensor([3000, 1234, 2049], dtype=torch.int32)
+    g = torch.Generator().manual_seed(block_size)
+    nb = (S2 + block_size - 1) // block_size
+    nblocks = B * nb + 5
+    perm = torch.randperm(nblocks, generator=g)
+    pool = torch.zeros((nblocks, block_size, 1, 128), dtype=torch.uint8).view(inputs.FP8)
+    pscale = torch.ones((nblocks, block_size))
+    bt = torch.full((B, nb + 1), -1, dtype=torch.int32)
+    kf = inp["k"].view(torch.uint8)
+    for b in range(B):
+        for j in range(nb):
+            page = int(perm[b * nb + j])
+            bt[b, j] = page
+            lo, hi = j * block_size, min(S2, (j + 1) * block_size)
+            pool.view(torch.uint8)[page, :hi - lo] = kf[b, lo:hi]
+            pscale[page, :hi - lo] = inp["key_scale"][b, lo:hi]
+    print(f"indexer PA block_size={block_size}", flush=True)
+    d = {k: v.to(gpu) for k, v in inp.items()}
+    ic, vc, lc = dsa.lightning_indexer(d["q"], d["k"], d["w"], key_scale=d["key_scale"],
+                                       actual_seq_lengths_key=lens_k.to(gpu), sparse_count=K,
+                                       return_value=True, return_logits=True)
+    ip, _, lp = dsa.lightning_indexer(d["q"], pool.to(gpu), d["w"], key_scale=pscale.to(gpu),
+                                      actual_seq_lengths_key=lens_k.to(gpu), block_table=bt.to(gpu),
+                                      layout_key="PA_BSND", sparse_count=K, return_logits=True)
+    torch.cuda.synchronize()
+    assert torch.equal(ip.cpu(), ic.cpu())
+    # and against the oracle run on the paged layout itself
+    ri, rs, _ = ref_indexer(inp["q"], pool, inp["w"], key_scale=pscale, actual_seq_lengths_key=lens_k,
+                            block_table=bt, layout_key="PA_BSND", sparse_count=K)
+    lp, lc = lp.cpu(), lc.cpu()
+    for b in range(B):
+        for t in range(S1):
+            n = int(torch.isfinite(rs[b, 0, t]).sum())  # keys row t sees (unseen ones are not written)
+            assert torch.equal(lp[b, t, :n], lc[b, t, :n]), (b, t)
+            _logit_close(lp[b, t, :n], rs[b, 0, t, :n])
+            gs = set(x for x in ri[b, t, 0].tolist() if x >= 0)
+            ts = set(x for x in ic.cpu()[b, t, 0].tolist() if x >= 0)
+            assert len(gs ^ ts) <= 2, (b, t)
+
+
+def test_tnd_query_with_paged_keys(gpu):
+    # decode-like: one or a few query rows per sequence (TND) over paged fp8 caches
+    lens_q, lens_k, K, bs = [1, 1, 3, 1], [5000, 70, 2048, 9000], 2048, 64
+    q, k, w, ks = _ragged_fp8(77, lens_q, lens_k)
+    nbs = [(x + bs - 1) // bs for x in lens_k]
+    nblocks = sum(nbs) + 2
+    g = torch.Generator().manual_seed(3)
+    perm = torch.randperm(nblocks, generator=g)
+    pool = torch.zeros((nblocks, bs, 1, 128), dtype=torch.uint8)
+    pscale = torch.ones((nblocks, bs))
+    bt = torch.full((4, max(nbs)), -1, dtype=torch.int32)
+    kf, off, pi = k.view(torch.uint8), 0, 0
+    for b, ak in enumerate(lens_k):
+        for j in range(nbs[b]):
+            page = int(perm[pi]); pi += 1
+            bt[b, j] = page
+            lo, hi = j * bs, min(ak, (j + 1) * bs)
+            pool[page, :hi - lo] = kf[off + lo:off + hi]
+            pscale[page, :hi - lo] = ks[off + lo:off + hi]
+        off += ak
+    pool = pool.view(inputs.FP8)
+    cq = _cum(lens_q)
+    print("indexer TND query + PA keys", flush=True)
+    idx, _, logits = dsa.lightning_indexer(q.to(gpu), pool.to(gpu), w.to(gpu), key_scale=pscale.to(gpu),
+                                           actual_seq_lengths_query=cq.to(gpu),
+                                           actual_seq_lengths_key=torch.tensor(lens_k).to(gpu),
+                                           block_table=bt.to(gpu), layout_query="TND", layout_key="PA_BSND",
+                                           sparse_count=K, return_logits=True)
+    torch.cuda.synchronize()
+    ri, rscores, _ = ref_indexer(q, pool, w, key_scale=pscale, actual_seq_lengths_query=cq,
+                                 actual_seq_lengths_key=torch.tensor(lens_k), block_table=bt,
+                                 layout_query="TND", layout_key="PA_BSND", sparse_count=K)
+    logits, idx = logits.cpu(), idx.cpu()
+    row = 0
+    for b, (aq, ak) in enumerate(zip(lens_q, lens_k)):
+        for t in range(aq):
+            ref = rscores[b, 0, t, :ak]
+            n = int(torch.isfinite(ref).sum())
+            _logit_close(logits[row, :n].unsqueeze(0), ref[:n].unsqueeze(0))
+            ti, _ = stable_topk(logits[row, :n].unsqueeze(0), K)
+            assert torch.equal(idx[row, 0], ti[0]), (b, t)
+            row += 1

@@ -116,3 +116,97 @@ def test_fp8_dequant_identity():
     kdq = k8.float() * scale.unsqueeze(-1)
     _, s_deq, _ = lightning_indexer(q.float(), kdq, w, sparse_count=4, sparse_mode=0)
     assert torch.allclose(s_fp8, s_deq, rtol=1e-5, atol=1e-4)
+
+
+def _varlen_case(seed, lens_q, lens_k, N1=4, D=128):
+    """Ragged batches: per-batch queries / keys, as a list of tensors."""
+    g = torch.Generator().manual_seed(seed)
+    qs = [torch.randn((aq, N1, D), generator=g) for aq in lens_q]
+    ks = [torch.randn((ak, 1, D), generator=g) for ak in lens_k]
+    ws = [torch.randn((aq, N1), generator=g) for aq in lens_q]
+    return qs, ks, ws
+
+
+def _cumsum(lens):
+    out, acc = [], 0
+    for x in lens:
+        acc += x
+        out.append(acc)
+    return torch.tensor(out, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("mode", [3, 0])
+def test_tnd_layout_vs_bruteforce(mode):
+    # TND query and key (lightning_indexer.py:48-84,111-150: prefix-sum lengths,
+    # output [T, N2, K]); every row checked against the triple loop of its batch
+    lens_q, lens_k, K = [3, 0, 5], [20, 7, 33], 12
+    qs, ks, ws = _varlen_case(21 + mode, lens_q, lens_k)
+    q, k, w = torch.cat(qs), torch.cat(ks), torch.cat(ws)
+    idx, _, vals = lightning_indexer(q, k, w, actual_seq_lengths_query=_cumsum(lens_q),
+                                     actual_seq_lengths_key=_cumsum(lens_k), layout_query="TND",
+                                     layout_key="TND", sparse_count=K, sparse_mode=mode)
+    assert idx.shape == (sum(lens_q), 1, K)
+    row = 0
+    for b, (aq, ak) in enumerate(zip(lens_q, lens_k)):
+        if aq == 0:
+            continue
+        ref = brute_scores(qs[b], ks[b][:, 0], ws[b], aq, ak, mode)
+        for t in range(aq):
+            r = ref[t].tolist()
+            order = sorted(range(ak), key=lambda i: (-r[i], i))[:K]
+            exp = [i if r[i] > -1e30 else -1 for i in order] + [-1] * (K - min(K, ak))
+            assert idx[row, 0].tolist() == exp, (b, t)
+            row += 1
+
+
+def test_tnd_equals_padded_bsnd():
+    # the padded form of the same ragged batches (BSND with per-batch lengths)
+    lens_q, lens_k, K = [4, 2], [30, 18], 8
+    qs, ks, ws = _varlen_case(5, lens_q, lens_k)
+    B, S1, S2 = 2, max(lens_q), max(lens_k)
+    qp = torch.zeros((B, S1, 4, 128))
+    kp = torch.zeros((B, S2, 1, 128))
+    wp = torch.zeros((B, S1, 4))
+    for b in range(B):
+        qp[b, :lens_q[b]] = qs[b]
+        kp[b, :lens_k[b]] = ks[b]
+        wp[b, :lens_q[b]] = ws[b]
+    ip, sp, _ = lightning_indexer(qp, kp, wp, actual_seq_lengths_query=torch.tensor(lens_q),
+                                  actual_seq_lengths_key=torch.tensor(lens_k), sparse_count=K)
+    it, st, _ = lightning_indexer(torch.cat(qs), torch.cat(ks), torch.cat(ws),
+                                  actual_seq_lengths_query=_cumsum(lens_q),
+                                  actual_seq_lengths_key=_cumsum(lens_k), layout_query="TND",
+                                  layout_key="TND", sparse_count=K)
+    row = 0
+    for b in range(B):
+        for t in range(lens_q[b]):
+            assert torch.equal(it[row, 0], ip[b, t, 0])
+            row += 1
+    assert torch.equal(torch.nan_to_num(st, neginf=-1.0), torch.nan_to_num(sp, neginf=-1.0))
+
+
+@pytest.mark.parametrize("block_size", [16, 64])
+def test_paged_keys_equal_contiguous(block_size):
+    # PA_BSND (lightning_indexer.py:271-292 golden gather bt[b, s // bs], s % bs):
+    # the keys scattered over a shuffled page pool give the contiguous result
+    g = torch.Generator().manual_seed(block_size)
+    B, S1, S2, K = 2, 5, 100, 16
+    q = torch.randn((B, S1, 4, 128), generator=g)
+    k = torch.randn((B, S2, 1, 128), generator=g)
+    w = torch.randn((B, S1, 4), generator=g)
+    lens_k = [100, 77]
+    nb = (S2 + block_size - 1) // block_size
+    perm = torch.randperm(B * nb + 3, generator=g)
+    pool = torch.randn((B * nb + 3, block_size, 1, 128), generator=g)
+    bt = torch.full((B, nb + 2), -1, dtype=torch.int32)
+    for b in range(B):
+        for j in range(nb):
+            page = int(perm[b * nb + j])
+            bt[b, j] = page
+            lo, hi = j * block_size, min(S2, (j + 1) * block_size)
+            pool[page, :hi - lo] = k[b, lo:hi]
+    ic, sc, _ = lightning_indexer(q, k, w, actual_seq_lengths_key=torch.tensor(lens_k), sparse_count=K)
+    ipa, spa, _ = lightning_indexer(q, pool, w, actual_seq_lengths_key=torch.tensor(lens_k), block_table=bt,
+                                    layout_key="PA_BSND", sparse_count=K)
+    assert torch.equal(ipa, ic)
+    assert torch.equal(torch.nan_to_num(spa, neginf=-1.0), torch.nan_to_num(sc, neginf=-1.0))

@@ -48,14 +48,20 @@ constexpr int kKeyLoaders = kTileBytes / 1024;   // waves 0..7 load 1 KB of keys
 constexpr int kScaleLoader = kKeyLoaders;        // wave 8 loads the tile's key scales
 constexpr int kSplits = 4;                       // fp8 pieces of u
 constexpr int kE4m3Max = 448;
+constexpr int kMaxChunk = 4096;                  // keys per workgroup at most
 
 struct IndexerParams {
   const uint8_t* q;        // [B, S1, 64, 128] fp8
   const uint8_t* k;        // [B, S2, 128] fp8
   const float* key_scale;  // [B, S2] or null
   const float* w;          // [B, S1, 64]
-  const int32_t* act_q;    // [B] or null
-  const int32_t* act_k;    // [B] or null
+  const int32_t* act_q;    // [B] per-batch query lengths or null
+  const int32_t* act_k;    // [B] per-batch key lengths or null
+  const int32_t* cum_q;    // [B] prefix sums of the query lengths (varlen rows) or null
+  const int32_t* cum_k;    // [B] prefix sums of the key lengths (varlen keys) or null
+  const int32_t* block_table;  // [B, max_blocks] pages of the key pool (paged keys) or null
+  int64_t pool_rows;       // keys in the page pool
+  int block_size, max_blocks;
   float* logits;           // [B * S1, ld]
   int32_t* row_len;        // [B * S1] or null
   int64_t ld;
@@ -109,8 +115,18 @@ __device__ __forceinline__ float lds_read_f32(uint32_t addr) {
   return v;
 }
 
+// Source of the key loads for pages outside the pool (never scored: such keys
+// only occur in malformed block tables, which the host wrapper rejects).
+__device__ __align__(16) uint8_t g_zero_key[kDim];
+__device__ float g_zero_scale[kKeyTile];
+
+// PAGED: keys live in a page pool [blocks * block_size, D] addressed through
+// p.block_table; the physical rows of this workgroup's key chunk are resolved
+// once into LDS.
+template <bool PAGED>
 __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) {
   __shared__ __align__(1024) uint8_t ktile[kStages][kTileBytes];
+  __shared__ int32_t krows[PAGED ? kMaxChunk : 1];
   __shared__ __align__(256) float kscale[kStages][kKeyTile];
   // u pieces, rows padded to 144 B so the 16 rows one MFMA operand read touches
   // fall on distinct banks
@@ -127,8 +143,23 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   if (kg >= p.B * p.nkc) return;
   const int b = kg / p.nkc, kc = kg % p.nkc;
 
-  const int aq = p.act_q ? clampi(p.act_q[b], 0, p.S1) : p.S1;
-  const int ak = p.act_k ? clampi(p.act_k[b], 0, p.S2) : p.S2;
+  // Rows of batch b: varlen (prefix sums) or padded [B, S1] / [B, S2].
+  int aq, ak;
+  int64_t qbase, kbase_row;
+  if (p.cum_q) {
+    qbase = b > 0 ? p.cum_q[b - 1] : 0;
+    aq = clampi(p.cum_q[b] - (int)qbase, 0, p.S1);
+  } else {
+    qbase = (int64_t)b * p.S1;
+    aq = p.act_q ? clampi(p.act_q[b], 0, p.S1) : p.S1;
+  }
+  if (p.cum_k) {
+    kbase_row = b > 0 ? p.cum_k[b - 1] : 0;
+    ak = clampi(p.cum_k[b] - (int)kbase_row, 0, p.S2);
+  } else {
+    kbase_row = (int64_t)b * p.S2;
+    ak = p.act_k ? clampi(p.act_k[b], 0, p.S2) : p.S2;
+  }
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -145,11 +176,12 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   const int k1 = min(kend, lmax);            // last key any token needs
 
   const int tok = tb * kTokPerBlock + wave;
-  const bool tok_ok = tok < p.S1;
+  // varlen rows past the batch's length do not exist; padded rows do (row_len 0)
+  const bool tok_ok = p.cum_q ? tok < aq : tok < p.S1;
   const int L = tok_ok ? visible_keys(tok, aq, ak, p.sparse_mode) : 0;
-  if (kc == 0 && p.row_len != nullptr && lane == 0 && tok_ok) p.row_len[(int64_t)b * p.S1 + tok] = L;
+  if (kc == 0 && p.row_len != nullptr && lane == 0 && tok_ok) p.row_len[qbase + tok] = L;
   if (k0 >= k1) return;
-  const int64_t trow = (int64_t)b * p.S1 + (tok_ok ? tok : 0);
+  const int64_t trow = qbase + (tok_ok ? tok : 0);
 
   // ---- per-token operands -------------------------------------------------
   // q: lane (g, c) holds head 16*mt + c, bytes [32g, 32g+32) of the head.
@@ -193,6 +225,16 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
     e = clampi(ex, -100, 100);
   }
   if (lane == 0) uexp[wave] = e;
+  if constexpr (PAGED) {
+    // physical pool row of every key of the chunk (-1: page outside the pool)
+    for (int i = tid; i < k1 - k0; i += kThreads) {
+      const int key = k0 + i;
+      const int blk = key / p.block_size;
+      const int pg = blk < p.max_blocks ? p.block_table[(int64_t)b * p.max_blocks + blk] : -1;
+      const int64_t row = (int64_t)pg * p.block_size + key % p.block_size;
+      krows[i] = (pg >= 0 && row < p.pool_rows) ? (int32_t)row : -1;
+    }
+  }
   {
     float r0 = u0, r1 = u1;
 #pragma unroll
@@ -215,8 +257,8 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
 
   // ---- key tiles ------------------------------------------------------------
   const int ntiles = (k1 - k0 + kKeyTile - 1) / kKeyTile;
-  const uint8_t* kbase = p.k + (int64_t)b * p.S2 * kDim;
-  const float* sbase = p.key_scale ? p.key_scale + (int64_t)b * p.S2 : nullptr;
+  const uint8_t* kbase = PAGED ? p.k : p.k + kbase_row * kDim;
+  const float* sbase = p.key_scale ? (PAGED ? p.key_scale : p.key_scale + kbase_row) : nullptr;
   const bool loader = wave < kKeyLoaders || (wave == kScaleLoader && sbase != nullptr);
   // Loader lane l of wave w fills LDS bytes [w KB + 16 l, +16) of a tile: key
   // s = 8w + l/8, slot l%8, which holds the key's chunk (l%8) ^ swz(s).
@@ -227,11 +269,14 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
     const int kt0 = k0 + t * kKeyTile;
     if (wave < kKeyLoaders) {
       const int key = min(kt0 + lkey, k1 - 1);
-      __builtin_amdgcn_global_load_lds(kbase + (int64_t)key * kDim + 16 * lchunk,
-                                       (DSA_LDS void*)&ktile[t & (kStages - 1)][1024 * wave], 16, 0, 0);
+      const int row = PAGED ? krows[key - k0] : key;
+      const uint8_t* src = row >= 0 ? kbase + (int64_t)row * kDim + 16 * lchunk : g_zero_key + 16 * lchunk;
+      __builtin_amdgcn_global_load_lds(src, (DSA_LDS void*)&ktile[t & (kStages - 1)][1024 * wave], 16, 0, 0);
     } else if (wave == kScaleLoader && sbase != nullptr) {
       const int key = min(kt0 + lane, k1 - 1);
-      __builtin_amdgcn_global_load_lds(sbase + key, (DSA_LDS void*)&kscale[t & (kStages - 1)][0], 4, 0, 0);
+      const int row = PAGED ? krows[key - k0] : key;
+      const float* src = row >= 0 ? sbase + row : g_zero_scale + lane;
+      __builtin_amdgcn_global_load_lds(src, (DSA_LDS void*)&kscale[t & (kStages - 1)][0], 4, 0, 0);
     }
   };
   // B-operand reads: lane (g, c) reads key 16blk + c, chunks 2g and 2g+1.
@@ -374,7 +419,9 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
 namespace dsa {
 
 int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scale, const float* w,
-                       const int32_t* act_q, const int32_t* act_k, int B, int S1, int S2,
+                       const int32_t* act_q, const int32_t* act_k, const int32_t* cum_q,
+                       const int32_t* cum_k, const int32_t* block_table, int block_size,
+                       int max_blocks, int64_t pool_rows, int B, int S1, int S2,
                        int sparse_mode, float* logits, int64_t ld, int32_t* row_len,
                        hipStream_t stream) {
   IndexerParams p;
@@ -384,6 +431,12 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
   p.w = w;
   p.act_q = act_q;
   p.act_k = act_k;
+  p.cum_q = cum_q;
+  p.cum_k = cum_k;
+  p.block_table = block_table;
+  p.block_size = block_size;
+  p.max_blocks = max_blocks;
+  p.pool_rows = pool_rows;
   p.logits = logits;
   p.row_len = row_len;
   p.ld = ld;
@@ -394,7 +447,7 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
   p.ntb = (S1 + kTokPerBlock - 1) / kTokPerBlock;
   // Aim for >= 4 workgroups per CU over the whole launch while keeping each
   // workgroup's key chunk a multiple of the LDS tile.
-  int chunk = 4096;
+  int chunk = kMaxChunk;
   while (chunk > kKeyTile && (int64_t)B * p.ntb * ((S2 + chunk - 1) / chunk) < 1024) chunk >>= 1;
   p.chunk = chunk;
   p.nkc = (S2 + chunk - 1) / chunk;
@@ -402,7 +455,10 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
   const int64_t nblocks = ((groups + kNumXcd - 1) / kNumXcd) * kNumXcd * p.ntb;
   if (nblocks <= 0) return kOk;
   if (nblocks > 0x7fffffff) return set_error(kUnsupported, "indexer: grid too large");
-  hipLaunchKernelGGL(indexer_fp8_kernel, dim3((unsigned)nblocks), dim3(kThreads), 0, stream, p);
+  if (block_table != nullptr)
+    hipLaunchKernelGGL(indexer_fp8_kernel<true>, dim3((unsigned)nblocks), dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL(indexer_fp8_kernel<false>, dim3((unsigned)nblocks), dim3(kThreads), 0, stream, p);
   return check_launch("dsa_indexer_logits_fp8");
 }
 
@@ -427,8 +483,9 @@ extern "C" int dsa_indexer_logits_fp8(const void* q, const void* k, const float*
   if (q == nullptr || k == nullptr || weights == nullptr || logits == nullptr)
     return set_error(kInvalidArgument, "dsa_indexer_logits_fp8: null pointer");
   return indexer_fp8_launch(static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(k),
-                            key_scale, weights, act_q, act_k, (int)B, (int)S1, (int)S2,
-                            sparse_mode, logits, ld, row_len, (hipStream_t)stream);
+                            key_scale, weights, act_q, act_k, nullptr, nullptr, nullptr, 0, 0, 0,
+                            (int)B, (int)S1, (int)S2, sparse_mode, logits, ld, row_len,
+                            (hipStream_t)stream);
 }
 
 namespace dsa {
@@ -470,4 +527,87 @@ extern "C" int dsa_lightning_indexer_fp8(const void* q, const void* k, const flo
                                   sparse_mode, logits, S2, row_len, stream);
   if (rc != kOk) return rc;
   return topk_launch(logits, B * S1, S2, S2, row_len, sparse_count, 1, indices, values, st);
+}
+
+extern "C" int dsa_indexer_logits_fp8_varlen(const void* q, const void* k, const float* key_scale,
+                                             const float* weights, const int32_t* seq_q,
+                                             int32_t seq_q_cumulative, const int32_t* seq_k,
+                                             int32_t seq_k_cumulative, const int32_t* block_table,
+                                             int32_t block_size, int32_t max_blocks, int64_t pool_rows,
+                                             int64_t B, int64_t S1, int64_t S2, int32_t N1, int32_t D,
+                                             int32_t sparse_mode, float* logits, int64_t ld,
+                                             int32_t* row_len, void* stream) {
+  using namespace dsa;
+  if (N1 != kHeads || D != kDim)
+    return set_error(kUnsupported,
+                     "dsa_indexer_logits_fp8_varlen: only 64 index heads x 128 dims are built (got %d x %d)", N1, D);
+  if (B < 0 || S1 < 0 || S2 < 0 || ld < S2 || S1 > 0x7fffffff || S2 > 0x7fffffff || B > 0x7fffffff)
+    return set_error(kInvalidArgument, "dsa_indexer_logits_fp8_varlen: bad sizes");
+  if (sparse_mode != 0 && sparse_mode != 3)
+    return set_error(kInvalidArgument, "dsa_indexer_logits_fp8_varlen: sparse_mode must be 0 or 3, got %d",
+                     sparse_mode);
+  if ((seq_q_cumulative && seq_q == nullptr) || (seq_k_cumulative && seq_k == nullptr))
+    return set_error(kInvalidArgument, "dsa_indexer_logits_fp8_varlen: cumulative lengths need a length array");
+  if (block_table != nullptr) {
+    if (block_size <= 0 || max_blocks <= 0 || pool_rows < 0 || pool_rows > 0x7fffffff)
+      return set_error(kInvalidArgument,
+                       "dsa_indexer_logits_fp8_varlen: paged keys need block_size > 0, max_blocks > 0 and "
+                       "pool_rows in [0, 2^31)");
+    if (seq_k_cumulative)
+      return set_error(kInvalidArgument,
+                       "dsa_indexer_logits_fp8_varlen: paged keys take per-batch key lengths, not prefix sums");
+  }
+  if (B == 0 || S1 == 0) return kOk;
+  if (q == nullptr || k == nullptr || weights == nullptr || logits == nullptr)
+    return set_error(kInvalidArgument, "dsa_indexer_logits_fp8_varlen: null pointer");
+  const int32_t* act_q = seq_q_cumulative ? nullptr : seq_q;
+  const int32_t* cum_q = seq_q_cumulative ? seq_q : nullptr;
+  const int32_t* act_k = seq_k_cumulative ? nullptr : seq_k;
+  const int32_t* cum_k = seq_k_cumulative ? seq_k : nullptr;
+  return indexer_fp8_launch(static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(k), key_scale,
+                            weights, act_q, act_k, cum_q, cum_k, block_table, block_size, max_blocks,
+                            pool_rows, (int)B, (int)S1, (int)S2, sparse_mode, logits, ld, row_len,
+                            (hipStream_t)stream);
+}
+
+extern "C" size_t dsa_lightning_indexer_varlen_workspace_bytes(int64_t q_rows, int64_t S2) {
+  return dsa_lightning_indexer_workspace_bytes(1, q_rows, S2);
+}
+
+extern "C" int dsa_lightning_indexer_fp8_varlen(const void* q, const void* k, const float* key_scale,
+                                                const float* weights, const int32_t* seq_q,
+                                                int32_t seq_q_cumulative, const int32_t* seq_k,
+                                                int32_t seq_k_cumulative, const int32_t* block_table,
+                                                int32_t block_size, int32_t max_blocks, int64_t pool_rows,
+                                                int64_t B, int64_t S1, int64_t S2, int64_t q_rows,
+                                                int32_t N1, int32_t D, int32_t sparse_count,
+                                                int32_t sparse_mode, int32_t* indices, float* values,
+                                                void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace dsa;
+  if (sparse_count < 1 || sparse_count > 8192)
+    return set_error(kInvalidArgument,
+                     "dsa_lightning_indexer_fp8_varlen: sparse_count must be in [1, 8192], got %d", sparse_count);
+  if (B < 0 || S1 < 0 || S2 < 0 || q_rows < 0)
+    return set_error(kInvalidArgument, "dsa_lightning_indexer_fp8_varlen: bad sizes");
+  if (!seq_q_cumulative && q_rows != B * S1)
+    return set_error(kInvalidArgument, "dsa_lightning_indexer_fp8_varlen: padded query rows need q_rows = B * S1");
+  if (q_rows == 0) return kOk;
+  const size_t need = dsa_lightning_indexer_varlen_workspace_bytes(q_rows, S2);
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(kWorkspaceTooSmall,
+                     "dsa_lightning_indexer_fp8_varlen: workspace of %zu bytes needed, %zu given", need,
+                     workspace_bytes);
+  if (indices == nullptr) return set_error(kInvalidArgument, "dsa_lightning_indexer_fp8_varlen: null indices");
+  float* logits = static_cast<float*>(workspace);
+  const size_t logit_bytes = (size_t)q_rows * S2 * sizeof(float);
+  int32_t* row_len =
+      reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + ((logit_bytes + 255) & ~size_t(255)));
+  hipStream_t st = (hipStream_t)stream;
+  if (S2 == 0 || B == 0 || S1 == 0)  // no keys (or no rows to score): every row is all -1
+    return topk_launch(logits, q_rows, 0, 0, nullptr, sparse_count, 1, indices, values, st);
+  int rc = dsa_indexer_logits_fp8_varlen(q, k, key_scale, weights, seq_q, seq_q_cumulative, seq_k,
+                                         seq_k_cumulative, block_table, block_size, max_blocks, pool_rows,
+                                         B, S1, S2, N1, D, sparse_mode, logits, S2, row_len, stream);
+  if (rc != kOk) return rc;
+  return topk_launch(logits, q_rows, S2, S2, row_len, sparse_count, 1, indices, values, st);
 }

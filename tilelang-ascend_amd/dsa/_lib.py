@@ -25,6 +25,13 @@ SIGNATURES = {
     "dsa_lightning_indexer_workspace_bytes": (c_sz, [c_i64, c_i64, c_i64]),
     "dsa_lightning_indexer_fp8": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                                           c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "dsa_indexer_logits_fp8_varlen": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32,
+                                              c_i32, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp,
+                                              c_i64, c_vp, c_vp]),
+    "dsa_lightning_indexer_varlen_workspace_bytes": (c_sz, [c_i64, c_i64]),
+    "dsa_lightning_indexer_fp8_varlen": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32,
+                                                 c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32,
+                                                 c_i32, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "dsa_sparse_mla_workspace_bytes": (c_sz, [c_i64, c_i64, c_i32, c_i32, c_i32]),
     "dsa_sparse_mla_fwd": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32,
                                    c_i32, c_i32, c_i64, c_i32, c_i32, c_i32, c_f32, c_i32, c_i32,

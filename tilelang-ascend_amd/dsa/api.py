@@ -131,10 +131,16 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
     (``torch.float8_e4m3fn``) with an optional per-key fp32 ``key_scale`` of shape
     ``[B, S2]`` (or ``[B, S2, 1]``); returned ``values`` are fp32.  ``block_n``,
     ``pp_slots`` and ``max_cores`` were Ascend tiling knobs and are accepted and
-    ignored.  Layouts: BSND query and key with N2 = 1.
-    Returns ``(indices int32 [B, S1, 1, sparse_count], values)``; ``values`` is an
-    empty tensor unless ``return_value``.  ``return_logits`` additionally returns
-    the fp32 logits ``[B, S1, S2]`` (valid for keys < the row's causal length).
+    ignored.  Layouts (N2 = 1): query BSND ``[B, S1, N1, D]`` or TND ``[T, N1, D]``
+    (``actual_seq_lengths_query`` = prefix sums); key BSND ``[B, S2, 1, D]``, TND
+    ``[T2, 1, D]`` (prefix sums) or PA_BSND ``[blocks, block_size, 1, D]`` with
+    ``block_table [B, max_blocks]`` and per-batch ``actual_seq_lengths_key``; the
+    key scale has the key's shape without D.  TND and paged keys are read in place
+    by the kernel (the reference pads and gathers them on the host first).
+    Returns ``(indices int32 [B, S1, 1, sparse_count] or [T, 1, sparse_count] for
+    TND, values)``; ``values`` is an empty tensor unless ``return_value``.
+    ``return_logits`` additionally returns the fp32 logits ``[B, S1, S2]`` (or
+    ``[T, S2]``), valid for keys below the row's causal length.
     """
     del block_n, pp_slots, max_cores
     if layout_query not in ("BSND", "TND"):
@@ -160,14 +166,93 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
         raise ValueError(f"query/key dtype must be float8_e4m3fn, got {query.dtype}")
     if weights.dtype != torch.float32:
         raise ValueError(f"weights dtype {weights.dtype} must be float32")
-    if layout_query != "BSND" or layout_key != "BSND" or block_table is not None:
-        raise NotImplementedError("only the BSND query/key layout is built")
-    if query.dim() != 4 or key.dim() != 4:
-        raise ValueError("BSND query and key must be 4-D [B, S, N, D]")
-    B, S1, N1, D = query.shape
-    Bk, S2, N2, Dk = key.shape
-    if Bk != B or Dk != D:
-        raise ValueError(f"key shape {tuple(key.shape)} does not match query {tuple(query.shape)}")
+    is_tnd = layout_query == "TND"
+    is_tnd_key = layout_key == "TND"
+    if is_tnd and actual_seq_lengths_query is None:
+        raise AssertionError("TND layout requires actual_seq_lengths_query (prefix sums)")
+    if is_pa and actual_seq_lengths_key is None:
+        raise AssertionError("PA_BSND case requires actual_seq_lengths")
+    if is_tnd_key and actual_seq_lengths_key is None:
+        raise AssertionError("TND layout requires actual_seq_lengths_key (prefix sums)")
+    if is_pa and block_table is None:
+        raise ValueError("PA_BSND layout requires block_table")
+    dev = _require_gpu(query, key, weights, key_scale, block_table)
+    for name, t in (("query", query), ("key", key), ("weights", weights)):
+        _require_contiguous(name, t)
+
+    # ---- query rows: BSND [B, S1, N1, D] or TND [T, N1, D] with prefix-sum lengths
+    if is_tnd:
+        if query.dim() != 3:
+            raise ValueError("TND query must be 3-D [T, N1, D]")
+        if actual_seq_lengths_query is None:
+            raise AssertionError("TND layout requires actual_seq_lengths_query (prefix sums)")
+        q_tot, N1, D = query.shape
+        cum_q = actual_seq_lengths_query.to(device=dev, dtype=torch.int32).contiguous()
+        B = cum_q.shape[0]
+        if B == 0 or int(cum_q[-1].item()) != q_tot:
+            raise ValueError(f"actual_seq_lengths_query must be prefix sums ending at T = {q_tot}")
+        q_lens = torch.diff(cum_q, prepend=torch.zeros(1, dtype=torch.int32, device=dev))
+        if bool((q_lens < 0).any()):
+            raise ValueError("actual_seq_lengths_query must be non-decreasing prefix sums")
+        S1 = int(q_lens.max().item())
+        if tuple(weights.shape) != (q_tot, N1):
+            raise ValueError(f"weights must be [T, N1] = {(q_tot, N1)}, got {tuple(weights.shape)}")
+        seq_q, seq_q_cum = cum_q, 1
+    else:
+        if query.dim() != 4:
+            raise ValueError("BSND query must be 4-D [B, S, N, D]")
+        B, S1, N1, D = query.shape
+        q_tot = B * S1
+        if tuple(weights.shape) != (B, S1, N1):
+            raise ValueError(f"weights must be [B, S1, N1] = {(B, S1, N1)}, got {tuple(weights.shape)}")
+        seq_q, seq_q_cum = _int32_vec("actual_seq_lengths_query", actual_seq_lengths_query, B, dev), 0
+
+    # ---- keys: BSND [B, S2, 1, D], TND [T2, 1, D] (prefix sums) or PA_BSND
+    # [blocks, block_size, 1, D] through block_table [B, max_blocks] (per-batch lengths)
+    bt, block_size, max_blocks, pool_rows = None, 0, 0, 0
+    if is_pa:
+        if key.dim() != 4:
+            raise ValueError("PA_BSND key must be 4-D [blocks, block_size, N2, D]")
+        nblk, block_size, N2, Dk = key.shape
+        if actual_seq_lengths_key is None:
+            raise AssertionError("PA_BSND case requires actual_seq_lengths")
+        if block_table is None:
+            raise ValueError("PA_BSND layout requires block_table")
+        if block_size % 16 != 0 or block_size > 1024 or block_size <= 0:
+            raise ValueError(f"PA block_size must be a positive multiple of 16 and <= 1024, got {block_size}")
+        if block_table.dim() != 2 or block_table.shape[0] != B:
+            raise ValueError(f"block_table must be [B, max_blocks], got {tuple(block_table.shape)}")
+        bt = block_table.to(device=dev, dtype=torch.int32).contiguous()
+        max_blocks, pool_rows = bt.shape[1], nblk * block_size
+        seq_k, seq_k_cum = actual_seq_lengths_key.to(device=dev, dtype=torch.int32).contiguous(), 0
+        if seq_k.numel() != B:
+            raise ValueError(f"actual_seq_lengths_key must have B = {B} entries, got {seq_k.numel()}")
+        S2 = int(seq_k.max().item()) if B > 0 else 0
+        k_tokens = pool_rows
+    elif is_tnd_key:
+        if key.dim() != 3:
+            raise ValueError("TND key must be 3-D [T2, N2, D]")
+        if actual_seq_lengths_key is None:
+            raise AssertionError("TND layout requires actual_seq_lengths_key (prefix sums)")
+        k_tot, N2, Dk = key.shape
+        seq_k, seq_k_cum = actual_seq_lengths_key.to(device=dev, dtype=torch.int32).contiguous(), 1
+        if seq_k.numel() != B or (B > 0 and int(seq_k[-1].item()) != k_tot):
+            raise ValueError(f"actual_seq_lengths_key must be {B} prefix sums ending at T2 = {k_tot}")
+        k_lens = torch.diff(seq_k, prepend=torch.zeros(1, dtype=torch.int32, device=dev))
+        if bool((k_lens < 0).any()):
+            raise ValueError("actual_seq_lengths_key must be non-decreasing prefix sums")
+        S2 = int(k_lens.max().item()) if B > 0 else 0
+        k_tokens = k_tot
+    else:
+        if key.dim() != 4:
+            raise ValueError("BSND key must be 4-D [B, S, N, D]")
+        Bk, S2, N2, Dk = key.shape
+        if Bk != B:
+            raise ValueError(f"key shape {tuple(key.shape)} does not match query batch {B}")
+        seq_k, seq_k_cum = _int32_vec("actual_seq_lengths_key", actual_seq_lengths_key, B, dev), 0
+        k_tokens = B * S2
+    if Dk != D:
+        raise ValueError(f"key head dim {Dk} does not match query head dim {D}")
     if D != 128:
         raise AssertionError(f"head dim must be 128, got {D}")
     if N2 != 1:
@@ -176,33 +261,29 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
         raise ValueError(f"query head_num (N1) must be <= 64, got {N1}")
     if N1 != 64:
         raise NotImplementedError(f"the fp8 kernel is built for N1 = 64 index heads, got {N1}")
-    if tuple(weights.shape) != (B, S1, N1):
-        raise ValueError(f"weights must be [B, S1, N1] = {(B, S1, N1)}, got {tuple(weights.shape)}")
-    dev = _require_gpu(query, key, weights, key_scale)
-    for name, t in (("query", query), ("key", key), ("weights", weights)):
-        _require_contiguous(name, t)
     ks = None
     if key_scale is not None:
-        if key_scale.numel() != B * S2:
-            raise ValueError(f"key_scale must have B*S2 = {B * S2} entries, got {key_scale.numel()}")
-        ks = key_scale.to(torch.float32).contiguous()
-    aq = _int32_vec("actual_seq_lengths_query", actual_seq_lengths_query, B, dev)
-    ak = _int32_vec("actual_seq_lengths_key", actual_seq_lengths_key, B, dev)
+        if key_scale.numel() != k_tokens:
+            raise ValueError(f"key_scale must have one entry per key token ({k_tokens}), got {key_scale.numel()}")
+        ks = key_scale.to(device=dev, dtype=torch.float32).contiguous()
 
-    indices = torch.empty((B, S1, 1, sparse_count), dtype=torch.int32, device=dev)
-    values = (torch.empty((B, S1, 1, sparse_count), dtype=torch.float32, device=dev)
-              if return_value else None)
+    out_shape = (q_tot, 1, sparse_count) if is_tnd else (B, S1, 1, sparse_count)
+    indices = torch.empty(out_shape, dtype=torch.int32, device=dev)
+    values = torch.empty(out_shape, dtype=torch.float32, device=dev) if return_value else None
     L = lib()
-    ws_bytes = L.dsa_lightning_indexer_workspace_bytes(B, S1, S2)
+    ws_bytes = L.dsa_lightning_indexer_varlen_workspace_bytes(q_tot, S2)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
-    check(L.dsa_lightning_indexer_fp8(_ptr(query), _ptr(key), _ptr(ks), _ptr(weights), _ptr(aq), _ptr(ak),
-                                      B, S1, S2, N1, D, sparse_count, sparse_mode, _ptr(indices),
-                                      _ptr(values), _ptr(ws), ws_bytes, _stream(dev)),
-          "dsa_lightning_indexer_fp8")
+    check(L.dsa_lightning_indexer_fp8_varlen(_ptr(query), _ptr(key), _ptr(ks), _ptr(weights), _ptr(seq_q), seq_q_cum,
+                                             _ptr(seq_k), seq_k_cum, _ptr(bt), block_size, max_blocks, pool_rows,
+                                             B, S1, S2, q_tot, N1, D, sparse_count, sparse_mode, _ptr(indices),
+                                             _ptr(values), _ptr(ws), ws_bytes, _stream(dev)),
+          "dsa_lightning_indexer_fp8_varlen")
     if values is None:
         values = torch.empty((0,), dtype=torch.float32, device=dev)
     if return_logits:
-        logits = ws[: B * S1 * S2 * 4].view(torch.float32).view(B, S1, S2)
+        logits = ws[: q_tot * S2 * 4].view(torch.float32).view(q_tot, S2)
+        if not is_tnd:
+            logits = logits.view(B, S1, S2)
         return indices, values, logits
     return indices, values
 
