@@ -87,3 +87,46 @@ def test_reference_factory_fp16_sentinel_convention(gpu):
     ro, _ = sparse_mla_fwd_gather(inp["q"], inp["kv"], inp["indices"], None, q_start_index_s=900,
                                   is_causal=True, p_dtype=torch.bfloat16)
     torch.testing.assert_close(out, ro, **OUT_TOL)
+
+
+@pytest.mark.parametrize("block_size", [64, 128])
+def test_paged_prefill_per_batch_lengths(gpu, block_size):
+    # paged KV for prefill with per-batch KV lengths, the reference's masked PA
+    # kernel (example_sparse_flash_attn_mask_pa.py:216-236,398-426): index i of batch
+    # b is valid when i != -1 and i <= kv_len[b] - S + s; the row is
+    # pool[block_table[b, i // block_size], i % block_size]
+    B, S, H, topk = 2, 48, 128, 512
+    kv_len = [3000, 1100]
+    g = torch.Generator().manual_seed(block_size)
+    nb = [(n + block_size - 1) // block_size for n in kv_len]
+    nblocks = sum(nb) + 3
+    pool = torch.randn((nblocks, block_size, 1, 576), generator=g).to(torch.bfloat16)
+    perm = torch.randperm(nblocks, generator=g)
+    bt = torch.full((B, max(nb) + 1), -1, dtype=torch.int32)
+    q = torch.randn((B, S, H, 576), generator=g).to(torch.bfloat16)
+    idx = torch.full((B, S, 1, topk), -1, dtype=torch.int32)
+    contig = torch.zeros((B, max(kv_len), 1, 576), dtype=torch.bfloat16)
+    pi = 0
+    for b in range(B):
+        for j in range(nb[b]):
+            bt[b, j] = int(perm[pi]); pi += 1
+            lo, hi = j * block_size, min(kv_len[b], (j + 1) * block_size)
+            contig[b, lo:hi] = pool[bt[b, j], :hi - lo]
+        for t in range(S):
+            vis = kv_len[b] - S + t + 1
+            sel = torch.randperm(vis, generator=g)[:topk]
+            idx[b, t, 0, :len(sel)] = sel.int()
+    idx[0, 3, 0, 7] = kv_len[0] - S + 3 + 5   # a future index: masked by the causal rule
+    print(f"mla paged prefill block_size={block_size} kv_len={kv_len}", flush=True)
+    kvl = torch.tensor(kv_len, dtype=torch.int32)
+    out, lse = dsa.sparse_mla_fwd(q.to(gpu), pool.to(gpu), idx.to(gpu), block_table=bt.to(gpu),
+                                  seq_len_kv=kvl.to(gpu), is_causal=True)
+    oc, lc = dsa.sparse_mla_fwd(q.to(gpu), contig.to(gpu), idx.to(gpu), seq_len_kv=kvl.to(gpu), is_causal=True)
+    torch.cuda.synchronize()
+    # the same rows in the same order: bit-identical to the contiguous layout
+    assert torch.equal(out.cpu(), oc.cpu()) and torch.equal(lse.cpu(), lc.cpu())
+    for b in range(B):
+        ro, rl = sparse_mla_fwd_gather(q[b:b + 1], pool, idx[b:b + 1], None, block_table=bt[b:b + 1],
+                                       q_start_index_s=kv_len[b] - S, is_causal=True, p_dtype=torch.bfloat16)
+        torch.testing.assert_close(out[b:b + 1].float().cpu(), ro, **OUT_TOL)
+        torch.testing.assert_close(lse[b:b + 1].cpu(), rl, **LSE_TOL)

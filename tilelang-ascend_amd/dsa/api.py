@@ -335,7 +335,8 @@ def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor,
     reference (examples/sparse_flash_attention/example_sparse_flash_attn.py:18-292)
     with the gather rule of examples/deepseek_v4/sparse_attention.py:171-198:
     ``-1`` and out-of-range indices are skipped; ``is_causal`` also skips indices
-    above ``q_start_index_s + s`` (default ``Skv - S``; per batch if a tensor).
+    above ``q_start_index_s + s`` (per batch if a tensor; default ``seq_len_kv[b] - S``,
+    or ``Skv - S`` without ``seq_len_kv``, as example_sparse_flash_attn_mask_pa.py:221).
     ``out [B, S, H, 512]`` bf16 and ``lse [B, S, H]`` fp32 (natural log,
     sparse_flash_mla_golden.py:147-149).  A row without a valid index gets
     out = 0 and lse = -inf.
