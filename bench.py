@@ -227,6 +227,36 @@ def target_configs(L, steps: int) -> dict:
     res["indexer_topk_32k"] = {"indexer_us": round(ui, 1), "topk_us": round(ut, 1),
                                "indexer_frac_of_fp8_peak": round(fi / ui / 1e6 / PEAK_FP8_TFLOPS, 4),
                                "topk_frac_of_hbm": round(tb / ut / 1e3 / PEAK_HBM_GBS, 4)}
+    del ix, logits, rl, idx
+    torch.cuda.empty_cache()
+
+    # the fp8 producers of the indexer's operands: a 128K-token key cache and the
+    # 4096-token query chunk (64 heads, scales folded into the weights); HBM bound
+    g = torch.Generator(device=dev).manual_seed(6)
+    kb = torch.randn((131072, IDX_DIM), generator=g, device=dev).to(torch.bfloat16)
+    k8 = torch.empty(kb.shape, dtype=torch.uint8, device=dev)
+    ks = torch.empty((131072,), dtype=torch.float32, device=dev)
+    qb = torch.randn((4096, IDX_HEADS, IDX_DIM), generator=g, device=dev).to(torch.bfloat16)
+    wq = torch.randn((4096, IDX_HEADS), generator=g, device=dev)
+    q8 = torch.empty(qb.shape, dtype=torch.uint8, device=dev)
+    wo = torch.empty_like(wq)
+
+    def kq():
+        chk(L.dsa_quant_fp8_rows(kb.data_ptr(), kb.shape[0], IDX_DIM, k8.data_ptr(), ks.data_ptr(), st), "kquant")
+
+    def qq():
+        chk(L.dsa_indexer_q_quant_fp8(qb.data_ptr(), wq.data_ptr(), 4096, IDX_HEADS, IDX_DIM, q8.data_ptr(),
+                                      wo.data_ptr(), st), "qquant")
+
+    uk = _time_launches(kq, steps)
+    uq = _time_launches(qq, steps)
+    kbytes = kb.numel() * 3 + ks.numel() * 4
+    qbytes = qb.numel() * 3 + wq.numel() * 8
+    res["fp8_producers"] = {"key_cache_128k_us": round(uk, 2),
+                            "key_cache_frac_of_hbm": round(kbytes / uk / 1e3 / PEAK_HBM_GBS, 4),
+                            "query_4096_us": round(uq, 2),
+                            "query_frac_of_hbm": round(qbytes / uq / 1e3 / PEAK_HBM_GBS, 4),
+                            "algorithmic_bytes": {"key_cache": kbytes, "query": qbytes}}
     return res
 
 

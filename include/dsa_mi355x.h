@@ -168,6 +168,46 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices,
                        void* out, float* lse, void* workspace, size_t workspace_bytes,
                        void* stream);
 
+/*
+ * Row quantisation (the step before the indexer).  x is bf16 [rows, cols],
+ * cols a multiple of 8, x 16-byte and y 8-byte aligned; one scale per row.
+ *
+ * dsa_act_quant_int8 replaces the call of act_quant_kernel_int8_optimized
+ * (examples/deepseek_v4/act_quant.py:25-90, outputs Y [M, N] int8 and S [M] fp32)
+ * with the golden's rule (act_quant_torch, :110-149): s = max(absmax, 1e-4) / 127
+ * (round_scale = 1: 2^ceil(log2 of it), the fast_round_scale bit rule of
+ * :93-107), y = round_half_even(clamp(x / s, -127, 127)).
+ *
+ * dsa_quant_fp8_rows: s = max(absmax / 448, FLT_MIN), y = e4m3fn(x / s) rounded
+ * to nearest even — the per-key fp8 quantisation whose scale is the indexer's
+ * key_scale (the fp8 producer of the lightning indexer,
+ * examples/deepseek_v4/lightning_indexer.py:199-335 consumes its dequantised form).
+ */
+int dsa_act_quant_int8(const void* x, int64_t M, int64_t N, int32_t round_scale, int8_t* y,
+                       float* scale, void* stream);
+int dsa_quant_fp8_rows(const void* x, int64_t rows, int64_t cols, void* y, float* scale,
+                       void* stream);
+
+/*
+ * Quantise-on-append for a paged fp8 key cache in the indexer's PA_BSND layout
+ * (pool [blocks, block_size, 1, D] + key_scale [blocks, block_size],
+ * lightning_indexer.py:271-292): new bf16 keys k [T, D] are quantised with the
+ * dsa_quant_fp8_rows rule and written to pool row slots[t] (= page * block_size
+ * + offset; -1 or >= pool_rows: dropped) together with their scale, in one pass.
+ */
+int dsa_indexer_k_append_fp8(const void* k, int64_t T, int32_t D, const int64_t* slots,
+                             int64_t pool_rows, void* pool, float* pool_scale, void* stream);
+
+/*
+ * Indexer query producer: bf16 q [T, N1, D] -> fp8 q8 [T, N1, D] with one scale
+ * per (token, head), folded into the head weights: weights_out[t, h] =
+ * weights[t, h] * s[t, h] (exact for the ReLU score, since
+ * w * ReLU(s * q8 . k) = (w * s) * ReLU(q8 . k) for s > 0), so the indexer takes
+ * q8 and weights_out unchanged (lightning_indexer.py:199-335).
+ */
+int dsa_indexer_q_quant_fp8(const void* q, const float* weights, int64_t T, int32_t N1, int32_t D,
+                            void* q8, float* weights_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

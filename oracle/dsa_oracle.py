@@ -390,6 +390,76 @@ def lse_combine(outs: Sequence[torch.Tensor], lses: Sequence[torch.Tensor]):
     return out, lse
 
 
+# ---------------------------------------------------------------------------
+# row quantisation (the producer of the indexer's fp8 operands; int8 act quant)
+# ---------------------------------------------------------------------------
+FP8_MAX = 448.0
+
+
+def pow2_ceil(v: torch.Tensor) -> torch.Tensor:
+    """``2 ** ceil(log2(v))`` for positive normal fp32 ``v``, exactly: the bit rule
+    of fast_log2_ceil / fast_pow2 (examples/deepseek_v4/act_quant.py:93-107),
+    exponent plus one when any mantissa bit is set.  The golden writes it as
+    ``2 ** torch.ceil(torch.log2(...))`` (:131-132); the two differ only where
+    fp32 log2 rounds a value just above a power of two down onto it."""
+    m, e = torch.frexp(v.to(torch.float32))           # v = m * 2^e, m in [0.5, 1)
+    k = torch.where(m == 0.5, e - 1, e)
+    return torch.ldexp(torch.ones_like(v, dtype=torch.float32), k)
+
+
+def act_quant_int8(x: torch.Tensor, round_scale: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-row int8 quantisation, ``act_quant_torch`` (act_quant.py:110-149):
+    ``s = max(absmax, 1e-4) / 127`` (power of two with ``round_scale``),
+    ``y = round(clamp(x / s, -127, 127))`` (round half to even).  2-D ``[M, N]`` ->
+    ``(y [M, N] int8, s [M, 1])``; 3-D ``[b, s, N]`` -> scales ``[b, s, 1]``."""
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1]).to(torch.float32)
+    amax = torch.clamp(x2.abs().amax(dim=1, keepdim=True), min=1e-4)
+    scales = amax / 127.0
+    if round_scale:
+        scales = pow2_ceil(scales)
+    y = torch.round(torch.clamp(x2 / scales, -127, 127)).to(torch.float16).to(torch.int8)
+    return y.view(shape), scales.view(*shape[:-1], 1)
+
+
+def quant_fp8_rows(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-row fp8 e4m3fn quantisation over the last dim:
+    ``s = max(absmax / 448, FLT_MIN)``, ``y = e4m3fn(x / s)`` (round to nearest even,
+    torch's float8 conversion).  Returns ``(y, s)`` with ``s`` of shape ``x.shape[:-1]``.
+    This is the key quantisation whose scale is the indexer's ``key_scale``."""
+    x32 = x.to(torch.float32)
+    s = torch.clamp(x32.abs().amax(dim=-1) / FP8_MAX, min=torch.finfo(torch.float32).tiny)
+    return (x32 / s.unsqueeze(-1)).to(torch.float8_e4m3fn), s
+
+
+def indexer_q_quant_fp8(q: torch.Tensor, weights: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Indexer query producer: one fp8 scale per (token, head) folded into the head
+    weights, ``w' = w * s``, so that ``w' * ReLU(q8 . k) = w * ReLU((s q8) . k)``
+    (the score of lightning_indexer.py:199-335 with the dequantised query)."""
+    q8, s = quant_fp8_rows(q)
+    return q8, weights.to(torch.float32) * s
+
+
+def fp8_e4m3fn_nearest(v: torch.Tensor) -> torch.Tensor:
+    """Brute-force round-to-nearest-even onto the finite e4m3fn grid (enumerates
+    the 254 finite codes); used to pin torch's float8 conversion on in-range values."""
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn)
+    grid = codes.to(torch.float32)
+    fin = torch.isfinite(grid)
+    grid, codes = grid[fin], codes[fin]
+    d = (v.to(torch.float32).reshape(-1, 1) - grid.reshape(1, -1)).abs()
+    best = d.min(dim=1, keepdim=True).values
+    cand = d == best
+    # a tie sits between two neighbours: prefer the even mantissa code, and keep
+    # the sign of v for zero
+    even = (codes.view(torch.uint8) & 1) == 0
+    pick = torch.where(cand & even, 1, 0) * 2 + cand.int()
+    out = codes[pick.argmax(dim=1)].view(torch.uint8).clone()
+    zero = (out & 0x7F) == 0  # rounded to zero: the sign follows v
+    out[zero] = torch.where(torch.signbit(v.reshape(-1)[zero]), 0x80, 0x00).to(torch.uint8)
+    return out.view(torch.float8_e4m3fn).view(v.shape)
+
+
 PINNED_BY = {
     "stable_topk": "brute force sorted(key=(-v, i)); known answers restated from "
                    "test_topk/test_sort (arange N=51 K=10, N=131); ties, +-0.0, -inf rows, "
@@ -402,4 +472,13 @@ PINNED_BY = {
                    "invariance; LSE == logsumexp (tests/test_oracle_mla.py)",
     "sparse_mla_fwd_dense": "agreement with the gather form and brute force",
     "lse_combine": "split a row's index set in two, combine == unsplit result",
+    "act_quant_int8/pow2_ceil": "the golden's torch formula (2**ceil(log2)) on random rows, "
+                   "the reference test's tolerance (act_quant.py:162-163), max |y| = 127 at the "
+                   "row maximum, |x - y s| <= s / 2, half-to-even ties on constructed rows, "
+                   "power-of-two bounds s/2 < v <= s (tests/test_oracle_quant.py)",
+    "quant_fp8_rows": "torch's float8 conversion against a brute-force nearest-even search "
+                   "over the e4m3fn grid for every bf16 value in range, max |y| = 448 at the "
+                   "row maximum, power-of-two equivariance, the indexer's key recipe",
+    "indexer_q_quant_fp8": "indexer scores with (q8, w s) equal those with the dequantised "
+                   "query s q8 and w, to fp32 rounding",
 }

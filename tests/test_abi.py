@@ -92,6 +92,13 @@ def test_host_side_rejections(L):
     # an empty problem is a no-op that succeeds
     empty = list(args); empty[7] = 0
     assert L.dsa_sparse_mla_fwd(*empty) == 0
+    # row quantisers: cols must be a multiple of 8; null slot map / weights; empty is a no-op
+    assert L.dsa_quant_fp8_rows(None, 4, 12, None, None, None) == 1
+    assert L.dsa_quant_fp8_rows(None, 4, 16, None, None, None) == 1
+    assert L.dsa_act_quant_int8(None, 0, 16, 0, None, None, None) == 0
+    assert L.dsa_indexer_k_append_fp8(None, 2, 128, None, 10, None, None, None) == 1
+    assert L.dsa_indexer_q_quant_fp8(None, None, 1, 64, 128, None, None, None) == 1
+    assert L.dsa_indexer_q_quant_fp8(None, None, 1, 0, 128, None, None, None) == 1
 
 
 def test_workspace_queries(L):

@@ -425,3 +425,128 @@ def sparse_attention_fwd(heads: int, dim: int, tail_dim: int, topk: int, kv_stri
         return sparse_mla_fwd(q, kv, indices, scale, is_causal=is_causal, return_lse=False)
 
     return kernel
+
+
+# ---------------------------------------------------------------------------
+# row quantisation (the producer of the indexer's fp8 operands; int8 act quant)
+# ---------------------------------------------------------------------------
+def _bf16_rows(name: str, x: torch.Tensor) -> torch.device:
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16, got {x.dtype}")
+    dev = _require_gpu(x)
+    _require_contiguous(name, x)
+    if x.dim() < 1 or x.shape[-1] % 8 != 0 or x.shape[-1] == 0:
+        raise ValueError(f"{name}: the last dimension must be a positive multiple of 8, got {tuple(x.shape)}")
+    return dev
+
+
+def act_quant(x: torch.Tensor, round_scale: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-row int8 quantisation with the outputs of ``act_quant_torch``
+    (examples/deepseek_v4/act_quant.py:110-149): bf16 ``x [M, N]`` or ``[b, s, N]``
+    -> ``(y int8 of x's shape, scales fp32 [M, 1] or [b, s, 1])`` with
+    ``s = max(absmax, 1e-4) / 127`` (a power of two with ``round_scale``) and
+    ``y = round_half_even(clamp(x / s, -127, 127))``."""
+    if x.dim() not in (2, 3):
+        raise ValueError(f"x must be 2-D or 3-D, got {x.dim()}-D")
+    dev = _bf16_rows("x", x)
+    N = x.shape[-1]
+    M = x.numel() // N
+    y = torch.empty(x.shape, dtype=torch.int8, device=dev)
+    s = torch.empty((*x.shape[:-1], 1), dtype=torch.float32, device=dev)
+    check(lib().dsa_act_quant_int8(_ptr(x), M, N, int(bool(round_scale)), _ptr(y), _ptr(s), _stream(dev)),
+          "dsa_act_quant_int8")
+    return y, s
+
+
+def act_quant_kernel_int8_optimized(N: int, block_M: int = 32, block_N: int = 32,
+                                    round_scale: bool = False) -> Callable:
+    """Factory with the signature of the reference kernel
+    (examples/deepseek_v4/act_quant.py:25-90), returning ``kernel(X [M, N] bf16) ->
+    (Y [M, N] int8, S [M] fp32)`` as its ``out_idx=[-2, -1]`` does.  The block sizes
+    only tile the reference's Ascend kernel and are accepted for compatibility;
+    the scale is per whole row either way (the golden's rule, :117-149)."""
+    if N % 8 != 0 or N <= 0:
+        raise ValueError(f"N must be a positive multiple of 8, got {N}")
+
+    def kernel(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        if x.dim() != 2 or x.shape[1] != N:
+            raise ValueError(f"X must be [M, {N}], got {tuple(x.shape)}")
+        y, s = act_quant(x, round_scale)
+        return y, s.view(-1)
+
+    return kernel
+
+
+def quant_fp8(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-row fp8 quantisation over the last dim: bf16 ``x [..., D]`` ->
+    ``(y float8_e4m3fn [..., D], scale fp32 [...])`` with
+    ``scale = max(absmax / 448, FLT_MIN)`` and ``y = e4m3fn(x / scale)`` (nearest
+    even).  Keys quantised this way are the indexer's ``key`` / ``key_scale``."""
+    dev = _bf16_rows("x", x)
+    if _FP8 is None:
+        raise RuntimeError("this torch build has no float8_e4m3fn dtype")
+    D = x.shape[-1]
+    y = torch.empty(x.shape, dtype=_FP8, device=dev)
+    s = torch.empty(x.shape[:-1], dtype=torch.float32, device=dev)
+    check(lib().dsa_quant_fp8_rows(_ptr(x), x.numel() // D, D, _ptr(y), _ptr(s), _stream(dev)),
+          "dsa_quant_fp8_rows")
+    return y, s
+
+
+def paged_slots(block_table: torch.Tensor, batch: torch.Tensor, positions: torch.Tensor,
+                block_size: int) -> torch.Tensor:
+    """Pool rows of key positions in a paged cache: ``block_table[b, p // block_size]
+    * block_size + p % block_size`` (the PA_BSND addressing of
+    examples/deepseek_v4/lightning_indexer.py:271-292); ``-1`` where the table has
+    no page.  int64, on the table's device."""
+    b = batch.to(device=block_table.device, dtype=torch.int64)
+    p = positions.to(device=block_table.device, dtype=torch.int64)
+    blk = p // block_size
+    ok = (blk < block_table.shape[1]) & (p >= 0)
+    page = block_table.long()[b, torch.where(ok, blk, 0)]
+    return torch.where(ok & (page >= 0), page * block_size + p % block_size, -1)
+
+
+def indexer_k_append_fp8(key: torch.Tensor, pool: torch.Tensor, pool_scale: torch.Tensor,
+                         slots: torch.Tensor) -> None:
+    """Quantise-on-append into a paged fp8 key cache: bf16 ``key [T, D]`` (or
+    ``[T, 1, D]``) is quantised as :func:`quant_fp8` does and written, with its
+    scale, to ``pool [blocks, block_size, 1, D]`` / ``pool_scale [blocks,
+    block_size]`` at pool rows ``slots [T]`` (see :func:`paged_slots`; ``-1`` and
+    rows past the pool are dropped).  The pool is the indexer's PA_BSND key."""
+    if pool.dtype != _FP8 or pool_scale.dtype != torch.float32:
+        raise ValueError("pool must be float8_e4m3fn and pool_scale float32")
+    dev = _bf16_rows("key", key)
+    _require_gpu(key, pool, pool_scale, slots)
+    D = key.shape[-1]
+    T = key.numel() // D
+    if pool.dim() != 4 or pool.shape[2] != 1 or pool.shape[3] != D:
+        raise ValueError(f"pool must be [blocks, block_size, 1, {D}], got {tuple(pool.shape)}")
+    if tuple(pool_scale.shape) != tuple(pool.shape[:2]):
+        raise ValueError(f"pool_scale must be {tuple(pool.shape[:2])}, got {tuple(pool_scale.shape)}")
+    _require_contiguous("pool", pool)
+    _require_contiguous("pool_scale", pool_scale)
+    if slots.numel() != T:
+        raise ValueError(f"slots must have T = {T} entries, got {slots.numel()}")
+    sl = slots.to(device=dev, dtype=torch.int64).contiguous()
+    rows = pool.shape[0] * pool.shape[1]
+    check(lib().dsa_indexer_k_append_fp8(_ptr(key), T, D, _ptr(sl), rows, _ptr(pool), _ptr(pool_scale),
+                                         _stream(dev)), "dsa_indexer_k_append_fp8")
+
+
+def indexer_q_quant_fp8(query: torch.Tensor, weights: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Indexer query producer: bf16 ``query [..., N1, D]`` -> fp8 ``q8`` with one scale
+    per (token, head) folded into fp32 ``weights [..., N1]``: returns ``(q8,
+    weights * scale)``, the operands :func:`lightning_indexer` takes."""
+    dev = _bf16_rows("query", query)
+    _require_gpu(query, weights)
+    if query.dim() < 2 or tuple(weights.shape) != tuple(query.shape[:-1]):
+        raise ValueError(f"weights must be query.shape[:-1] = {tuple(query.shape[:-1])}, got {tuple(weights.shape)}")
+    N1, D = query.shape[-2], query.shape[-1]
+    T = query.numel() // (N1 * D)
+    w = weights.to(torch.float32).contiguous()
+    q8 = torch.empty(query.shape, dtype=_FP8, device=dev)
+    wo = torch.empty(w.shape, dtype=torch.float32, device=dev)
+    check(lib().dsa_indexer_q_quant_fp8(_ptr(query), _ptr(w), T, N1, D, _ptr(q8), _ptr(wo), _stream(dev)),
+          "dsa_indexer_q_quant_fp8")
+    return q8, wo
