@@ -64,6 +64,9 @@ class Layer:
         self.kv = (torch.randn((1, S2, 1, DQK), generator=g, device=dev) * 0.5).to(torch.bfloat16)
         self.logits = torch.empty((S1, S2), dtype=torch.float32, device=dev)
         self.row_len = torch.empty((S1,), dtype=torch.int32, device=dev)
+        # maxima of 16-key groups, emitted by the indexer and read by the top-k
+        self.ld_g = (S2 + 15) // 16
+        self.gmax = torch.empty((S1, self.ld_g), dtype=torch.float32, device=dev)
         self.idx = torch.empty((1, S1, 1, TOPK), dtype=torch.int32, device=dev)
         self.out = torch.empty((1, S1, H, DV), dtype=torch.bfloat16, device=dev)
         self.lse = torch.empty((1, S1, H), dtype=torch.float32, device=dev)
@@ -76,6 +79,7 @@ class Layer:
         self.dw = torch.randn((1, dec_b, IDX_HEADS), generator=g, device=dev) / 8
         self.dlogits = torch.empty((dec_b, S2), dtype=torch.float32, device=dev)
         self.drow = torch.empty((dec_b,), dtype=torch.int32, device=dev)
+        self.dgmax = torch.empty((dec_b, self.ld_g), dtype=torch.float32, device=dev)
         self.didx = torch.empty((dec_b, 1, 1, TOPK), dtype=torch.int32, device=dev)
         self.dq = (torch.randn((dec_b, 1, H, DQK), generator=g, device=dev) * 0.5).to(torch.bfloat16)
         self.dout = torch.empty((dec_b, 1, H, DV), dtype=torch.bfloat16, device=dev)
@@ -94,26 +98,28 @@ class Layer:
     def launch(self, i: int):
         L, st = self.L, self.stream
         if i == 0:
-            self._chk(L.dsa_indexer_logits_fp8(self.iq.data_ptr(), self.ik.data_ptr(), self.iks.data_ptr(),
-                                               self.iw.data_ptr(), None, None, 1, self.S1, self.S2, IDX_HEADS,
-                                               IDX_DIM, 3, self.logits.data_ptr(), self.S2,
-                                               self.row_len.data_ptr(), st), "indexer")
+            self._chk(L.dsa_indexer_logits_fp8_group_max(
+                self.iq.data_ptr(), self.ik.data_ptr(), self.iks.data_ptr(), self.iw.data_ptr(), None, None, 1,
+                self.S1, self.S2, IDX_HEADS, IDX_DIM, 3, self.logits.data_ptr(), self.S2, self.row_len.data_ptr(),
+                self.gmax.data_ptr(), self.ld_g, st), "indexer")
         elif i == 1:
-            self._chk(L.dsa_topk_f32(self.logits.data_ptr(), self.S1, self.S2, self.S2, self.row_len.data_ptr(),
-                                     TOPK, 1, self.idx.data_ptr(), None, st), "topk")
+            self._chk(L.dsa_topk_f32_group_max(self.logits.data_ptr(), self.S1, self.S2, self.S2,
+                                               self.row_len.data_ptr(), self.gmax.data_ptr(), self.ld_g, TOPK, 1,
+                                               self.idx.data_ptr(), None, st), "topk")
         elif i == 2:
             self._chk(L.dsa_sparse_mla_fwd(self.q.data_ptr(), self.kv.data_ptr(), self.idx.data_ptr(), None, None,
                                            self.q_start.data_ptr(), None, 1, self.S1, H, DQK, DV, self.S2, 0, 0,
                                            TOPK, DQK ** -0.5, 1, 0, self.out.data_ptr(), self.lse.data_ptr(),
                                            self.ws.data_ptr(), self.ws.numel(), st), "mla")
         elif i == 3:
-            self._chk(L.dsa_indexer_logits_fp8(self.dq_idx.data_ptr(), self.ik.data_ptr(), self.iks.data_ptr(),
-                                               self.dw.data_ptr(), None, None, 1, self.dec_b, self.S2, IDX_HEADS,
-                                               IDX_DIM, 0, self.dlogits.data_ptr(), self.S2,
-                                               self.drow.data_ptr(), st), "dec_indexer")
+            self._chk(L.dsa_indexer_logits_fp8_group_max(
+                self.dq_idx.data_ptr(), self.ik.data_ptr(), self.iks.data_ptr(), self.dw.data_ptr(), None, None, 1,
+                self.dec_b, self.S2, IDX_HEADS, IDX_DIM, 0, self.dlogits.data_ptr(), self.S2, self.drow.data_ptr(),
+                self.dgmax.data_ptr(), self.ld_g, st), "dec_indexer")
         elif i == 4:
-            self._chk(L.dsa_topk_f32(self.dlogits.data_ptr(), self.dec_b, self.S2, self.S2, self.drow.data_ptr(),
-                                     TOPK, 1, self.didx.data_ptr(), None, st), "dec_topk")
+            self._chk(L.dsa_topk_f32_group_max(self.dlogits.data_ptr(), self.dec_b, self.S2, self.S2,
+                                               self.drow.data_ptr(), self.dgmax.data_ptr(), self.ld_g, TOPK, 1,
+                                               self.didx.data_ptr(), None, st), "dec_topk")
         elif i == 5:
             self._chk(L.dsa_sparse_mla_fwd(self.dq.data_ptr(), self.pool.data_ptr(), self.didx.data_ptr(),
                                            self.bt.data_ptr(), self.dlen.data_ptr(), None, None, self.dec_b, 1, H,

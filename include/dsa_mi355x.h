@@ -61,6 +61,23 @@ int dsa_topk_f32(const float* scores, int64_t rows, int64_t cols, int64_t ld,
                  float* out_val, void* stream);
 
 /*
+ * The same top-k given, for each row, an upper bound of the maximum of every
+ * group of 16 consecutive scores: group_max [rows, ld_g] fp32, ld_g >=
+ * ceil(cols / 16), group_max[r, g] >= max(scores[r, 16g : 16g + 16] within the
+ * row length) (NaN ignored; -inf for an empty group).  The K-th largest group
+ * maximum bounds the K-th largest score from below, so only the groups reaching
+ * it are read.  The lightning indexer emits exact group maxima with its logits
+ * and selects through this path (the fused indexer -> top-k of
+ * examples/deepseek_v4/lightning_indexer.py:945-1036, where the block sort runs
+ * on the logits the Cube unit just produced).  Rows of fewer than 2 k groups,
+ * or whose groups reaching the bound are too many, fall back to reading the
+ * whole row; the result equals dsa_topk_f32's.
+ */
+int dsa_topk_f32_group_max(const float* scores, int64_t rows, int64_t cols, int64_t ld,
+                           const int32_t* row_len, const float* group_max, int64_t ld_g, int32_t k,
+                           int32_t pad_invalid, int32_t* out_idx, float* out_val, void* stream);
+
+/*
  * Lightning-indexer logits, fp8 e4m3 q and k with a per-key fp32 scale.
  * Replaces the Cube QK + ReLU and Vector weight/head-reduce/mask stages of the
  * `call` built by make_lightning_indexer_kernel
@@ -78,6 +95,18 @@ int dsa_indexer_logits_fp8(const void* q, const void* k, const float* key_scale,
                            int64_t B, int64_t S1, int64_t S2, int32_t N1, int32_t D,
                            int32_t sparse_mode, float* logits, int64_t ld, int32_t* row_len,
                            void* stream);
+
+/*
+ * The same logits plus, per query row, the maximum of every group of 16
+ * consecutive keys: group_max [B * S1, ld_g] fp32, ld_g >= ceil(S2 / 16) (groups
+ * past a row's visible keys hold -inf or are not written).  This is the input
+ * of dsa_topk_f32_group_max; dsa_lightning_indexer_fp8 chains the two.
+ */
+int dsa_indexer_logits_fp8_group_max(const void* q, const void* k, const float* key_scale,
+                                     const float* weights, const int32_t* act_q, const int32_t* act_k,
+                                     int64_t B, int64_t S1, int64_t S2, int32_t N1, int32_t D,
+                                     int32_t sparse_mode, float* logits, int64_t ld, int32_t* row_len,
+                                     float* group_max, int64_t ld_g, void* stream);
 
 /*
  * Full lightning indexer: logits (above) then top-`sparse_count` per query row.

@@ -103,8 +103,11 @@ def test_host_side_rejections(L):
 
 def test_workspace_queries(L):
     rows, S2 = 4096, 32768
-    logit_bytes = rows * S2 * 4
-    assert L.dsa_lightning_indexer_workspace_bytes(1, rows, S2) == ((logit_bytes + 255) // 256) * 256 + rows * 4
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    # logits | row lengths | maxima of 16-key groups
+    want = up(rows * S2 * 4) + up(rows * 4) + rows * (S2 // 16) * 4
+    assert L.dsa_lightning_indexer_workspace_bytes(1, rows, S2) == want
+    assert L.dsa_lightning_indexer_varlen_workspace_bytes(rows, S2) == want
     assert L.dsa_lightning_indexer_workspace_bytes(0, rows, S2) == 0
     # prefill (many tokens): no split, no workspace
     assert L.dsa_sparse_mla_workspace_bytes(1, 4096, 128, 2048, 0) == 0

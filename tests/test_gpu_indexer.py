@@ -236,3 +236,28 @@ def test_tnd_query_with_paged_keys(gpu):
             ti, _ = stable_topk(logits[row, :n].unsqueeze(0), K)
             assert torch.equal(idx[row, 0], ti[0]), (b, t)
             row += 1
+
+
+@pytest.mark.parametrize("S2,mode", [(131072, 3), (70000, 0)])
+def test_long_rows_group_max_selection(gpu, S2, mode):
+    # rows of >= 2 K groups of 16 keys: the indexer emits the group maxima and the
+    # top-k reads only the groups that can hold a top-K key; the indices equal the
+    # stable top-k of the same GPU logits (and the logits-only + plain top-k run)
+    inp = inputs.indexer_fp8(B=1, S1=24, S2=S2, seed=S2 + mode)
+    d = {k: v.to(gpu) for k, v in inp.items()}
+    print(f"indexer long rows S2={S2} mode={mode}", flush=True)
+    idx, vals, logits = dsa.lightning_indexer(d["q"], d["k"], d["w"], key_scale=d["key_scale"], sparse_count=2048,
+                                              sparse_mode=mode, return_value=True, return_logits=True)
+    torch.cuda.synchronize()
+    lg = logits.cpu().view(24, S2)
+    L = torch.tensor([S2 - 24 + t + 1 if mode == 3 else S2 for t in range(24)], dtype=torch.int32)
+    ti, tv = stable_topk(lg, 2048, row_len=L)
+    assert torch.equal(idx.cpu().view(24, -1), ti)
+    assert torch.equal(vals.cpu().view(24, -1), tv)
+    # a few rows' logits against the oracle
+    kdq = inp["k"].float() * inp["key_scale"].view(1, -1, 1, 1)
+    for t in (0, 23):
+        n = int(L[t])
+        qk = torch.relu(torch.einsum("hd,sd->hs", inp["q"][0, t].float(), kdq[0, :n, 0]))
+        ref = (inp["w"][0, t].unsqueeze(1) * qk).sum(0)
+        _logit_close(lg[t, :n], ref)

@@ -104,3 +104,53 @@ def test_simple_topk_selector_factory(gpu):
     # the reference example's check (example_topk_selector.py:61-86): per-row set equality
     for r in range(64):
         assert set(idx[r].tolist()) == set(ref[r].tolist())
+
+
+def _group_max(x, row_len=None):
+    # exact maxima of 16-element groups within each row's length (NaN ignored,
+    # -inf for groups past it), the bound the indexer emits
+    R, N = x.shape
+    ng = (N + 15) // 16
+    pad = torch.full((R, ng * 16), float("-inf"))
+    pad[:, :N] = x
+    if row_len is not None:
+        pad[torch.arange(ng * 16)[None, :] >= row_len[:, None].long()] = float("-inf")
+    pad = torch.where(torch.isnan(pad), torch.tensor(float("-inf")), pad)
+    return pad.view(R, ng, 16).amax(dim=-1).contiguous()
+
+
+@pytest.mark.parametrize("cols,k", [(131072, 2048), (70001, 2048), (65536, 512), (40000, 1024)])
+def test_group_max_path(gpu, cols, k):
+    # the threshold from group maxima, then only the groups reaching it are read;
+    # rows of fewer than 2 k groups take the streamed path: identical results
+    g = torch.Generator().manual_seed(cols + k)
+    x = torch.randn((6, cols), generator=g)
+    x[1] = torch.round(x[1] * 4) / 4                  # tie groups
+    x[2, ::5] = float("nan")
+    x[3, : cols // 2] = float("-inf")                 # half the row masked
+    x[4] = -x[4].abs()                                # all negative; zeros below
+    x[4, 100:140] = -0.0
+    x[5, 7::16] = 50.0 + torch.arange(len(range(7, cols, 16))) * 1e-3  # one large value per group
+    row_len = torch.tensor([cols, cols - 5, cols, cols, cols - 17, cols], dtype=torch.int32)
+    gm = _group_max(x, row_len)
+    print(f"topk group-max case cols={cols} k={k}", flush=True)
+    gi, gv = dsa.topk_selector(x.to(gpu), k, row_len=row_len.to(gpu), group_max=gm.to(gpu), return_values=True)
+    torch.cuda.synchronize()
+    ri, rv = stable_topk(x, k, row_len=row_len)
+    _assert_exact(gi.cpu(), gv.cpu(), ri, rv)
+
+
+def test_group_max_overflow_and_loose_bounds(gpu):
+    # every group reaching the bound (a constant row): the group list overflows
+    # and the exact passes decide; bounds above the true maxima stay correct
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn((3, 131072), generator=g)
+    x[0] = 1.0
+    gm = _group_max(x)
+    gm[1] += 0.5                                      # loose upper bounds
+    gm[2, ::3] = float("inf")
+    print("topk group-max overflow / loose bounds", flush=True)
+    gi, gv = dsa.topk_selector(x.to(gpu), 2048, group_max=gm.to(gpu), return_values=True)
+    torch.cuda.synchronize()
+    ri, rv = stable_topk(x, 2048)
+    _assert_exact(gi.cpu(), gv.cpu(), ri, rv)

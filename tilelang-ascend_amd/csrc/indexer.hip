@@ -64,7 +64,9 @@ struct IndexerParams {
   int block_size, max_blocks;
   float* logits;           // [B * S1, ld]
   int32_t* row_len;        // [B * S1] or null
+  float* gmax;             // [B * S1, ld_g] maxima of 16-key groups of the logits, or null
   int64_t ld;
+  int64_t ld_g;
   int B, S1, S2, sparse_mode;
   int chunk, ntb, nkc;
 };
@@ -292,6 +294,15 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   float* orow = p.logits + trow * p.ld + k0;
   const __amdgpu_buffer_rsrc_t ost = __builtin_amdgcn_make_buffer_rsrc(
       orow, (short)0, tok_ok ? (kend - k0) * 4 : 0, 0x00020000);
+  // Group maxima: one float per 16 keys (the chunk start is a multiple of 64).
+  const bool want_gmax = p.gmax != nullptr;
+  // Group maxima of four consecutive tiles are gathered in one register (lane
+  // 16 j + s holds group j of tile 4 b + s) and stored together.
+  const int gslot_lane = lane & 15;
+  float gacc = 0.f;
+  const __amdgpu_buffer_rsrc_t gst = __builtin_amdgcn_make_buffer_rsrc(
+      want_gmax ? p.gmax + trow * p.ld_g + k0 / 16 : p.logits, (short)0,
+      (want_gmax && tok_ok) ? ((kend - k0 + 15) / 16) * 4 : 0, 0x00020000);
 
   // The operand loads above complete before the ring starts, so the only vector
   // memory operations in flight inside the loop are the ring's and the stores.
@@ -307,8 +318,9 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   // Epilogue of a finished tile: reduce-scatter of the partial sums, plus u.k,
   // times the key scale, masked, stored.  tile < 0 issues a store that the
   // buffer range check drops, so every iteration has exactly one store.
-  auto finish = [&](const float (&ap)[4], float ksp, int tile, auto LB) {
+  auto finish = [&](const float (&ap)[4], float ksp, int tile, auto LB, auto SLOT) {
     constexpr uint32_t lin_off = decltype(LB)::value * kLinBuf;
+    constexpr int kSlot = decltype(SLOT)::value;  // tile % 4, or -1: the last tile (run-time slot)
     float r02, r13;
     {
       const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ap[0]), __float_as_uint(ap[2]), false, false);
@@ -328,6 +340,32 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
       voff = (tile * kKeyTile + lane) * 4;
     }
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sum), ost, voff, 0, 0);
+    if (want_gmax) {
+      // max over each row of 16 lanes (16 consecutive keys): v_max_f32 with DPP
+      // quad swaps, then half-row and row mirrors (each DPP source written two
+      // wait states earlier).  v_max_f32 returns the non-NaN operand, and the
+      // top-k orders NaN last, so a NaN logit never raises a group's maximum.
+      float m = sum;
+      asm volatile(
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf"
+          : "+v"(m));
+      const int slot = kSlot >= 0 ? kSlot : (tile & 3);
+      gacc = gslot_lane == slot ? m : gacc;
+      if (kSlot == 3 || kSlot < 0) {
+        // lanes 16 j + s, s <= slot, store group j of tile (tile - slot + s); the
+        // other lanes' offsets are out of range (dropped), as are tiles < 0
+        const int t = tile - slot + gslot_lane;
+        const int goff = (gslot_lane <= slot && t >= 0) ? (t * 4 + (lane >> 4)) * 4 : 0x40000000;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gacc), gst, goff, 0, 0);
+      }
+    }
   };
 
   const dsa::f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -339,8 +377,10 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
     constexpr int ST = decltype(STC)::value;
     constexpr uint32_t so = ST * kTileBytes;
     // This wave's load of tile `it` is done once at most min(2 + it, 5) newer
-    // memory operations (loads of later tiles, logit stores) are in flight; its
-    // LDS writes and reads of the previous iteration are complete.
+    // memory operations are in flight (the loads of the next two tiles, one logit
+    // store per finished tile; a group-maxima store every fourth tile only adds
+    // to them, so the bound stays safe); its LDS writes and reads of the previous
+    // iteration are complete.
     if (loader) wait_vmcnt_upto(min(kStages - 2 + it, 2 * kStages - 3));
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ksp));
     __builtin_amdgcn_s_barrier();
@@ -371,7 +411,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)  // D[row = head 16mt + 4g + i][col = key 16blk + c]
         d[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[mt], bf, zero, 0, 0, 0, 127, 0, 127);
-      if constexpr (blk == 0) finish(ap, ksp, it - 1, dsa::IntC<(ST + 1) & 1>{});
+      if constexpr (blk == 0) finish(ap, ksp, it - 1, dsa::IntC<(ST + 1) & 1>{}, dsa::IntC<(ST + 3) & 3>{});
       float acc = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
@@ -407,8 +447,8 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   __builtin_amdgcn_s_setprio(0);
   {
     const int last = ntiles - 1;
-    if (last & 1) finish(ap, ksp, last, dsa::IntC<1>{});
-    else finish(ap, ksp, last, dsa::IntC<0>{});
+    if (last & 1) finish(ap, ksp, last, dsa::IntC<1>{}, dsa::IntC<-1>{});
+    else finish(ap, ksp, last, dsa::IntC<0>{}, dsa::IntC<-1>{});
   }
   // No LDS DMA may still be in flight when the workgroup's LDS is released.
   if (loader) dsa::wait_vmcnt<0>();
@@ -423,7 +463,7 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
                        const int32_t* cum_k, const int32_t* block_table, int block_size,
                        int max_blocks, int64_t pool_rows, int B, int S1, int S2,
                        int sparse_mode, float* logits, int64_t ld, int32_t* row_len,
-                       hipStream_t stream) {
+                       float* gmax, int64_t ld_g, hipStream_t stream) {
   IndexerParams p;
   p.q = q;
   p.k = k;
@@ -439,7 +479,9 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
   p.pool_rows = pool_rows;
   p.logits = logits;
   p.row_len = row_len;
+  p.gmax = gmax;
   p.ld = ld;
+  p.ld_g = ld_g;
   p.B = B;
   p.S1 = S1;
   p.S2 = S2;
@@ -464,11 +506,11 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
 
 }  // namespace dsa
 
-extern "C" int dsa_indexer_logits_fp8(const void* q, const void* k, const float* key_scale,
-                                      const float* weights, const int32_t* act_q,
-                                      const int32_t* act_k, int64_t B, int64_t S1, int64_t S2,
-                                      int32_t N1, int32_t D, int32_t sparse_mode, float* logits,
-                                      int64_t ld, int32_t* row_len, void* stream) {
+namespace {
+int indexer_logits_impl(const void* q, const void* k, const float* key_scale, const float* weights,
+                        const int32_t* act_q, const int32_t* act_k, int64_t B, int64_t S1, int64_t S2,
+                        int32_t N1, int32_t D, int32_t sparse_mode, float* logits, int64_t ld,
+                        int32_t* row_len, float* gmax, int64_t ld_g, void* stream) {
   using namespace dsa;
   if (N1 != kHeads || D != kDim)
     return set_error(kUnsupported,
@@ -484,20 +526,66 @@ extern "C" int dsa_indexer_logits_fp8(const void* q, const void* k, const float*
     return set_error(kInvalidArgument, "dsa_indexer_logits_fp8: null pointer");
   return indexer_fp8_launch(static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(k),
                             key_scale, weights, act_q, act_k, nullptr, nullptr, nullptr, 0, 0, 0,
-                            (int)B, (int)S1, (int)S2, sparse_mode, logits, ld, row_len,
+                            (int)B, (int)S1, (int)S2, sparse_mode, logits, ld, row_len, gmax, ld_g,
                             (hipStream_t)stream);
+}
+}  // namespace
+
+extern "C" int dsa_indexer_logits_fp8(const void* q, const void* k, const float* key_scale,
+                                      const float* weights, const int32_t* act_q,
+                                      const int32_t* act_k, int64_t B, int64_t S1, int64_t S2,
+                                      int32_t N1, int32_t D, int32_t sparse_mode, float* logits,
+                                      int64_t ld, int32_t* row_len, void* stream) {
+  return indexer_logits_impl(q, k, key_scale, weights, act_q, act_k, B, S1, S2, N1, D, sparse_mode, logits,
+                             ld, row_len, nullptr, 0, stream);
+}
+
+extern "C" int dsa_indexer_logits_fp8_group_max(const void* q, const void* k, const float* key_scale,
+                                                const float* weights, const int32_t* act_q,
+                                                const int32_t* act_k, int64_t B, int64_t S1, int64_t S2,
+                                                int32_t N1, int32_t D, int32_t sparse_mode, float* logits,
+                                                int64_t ld, int32_t* row_len, float* group_max, int64_t ld_g,
+                                                void* stream) {
+  using namespace dsa;
+  if (group_max == nullptr || ld_g < (S2 + 15) / 16)
+    return set_error(kInvalidArgument, "dsa_indexer_logits_fp8_group_max: group_max with ld_g >= ceil(S2 / 16) needed");
+  return indexer_logits_impl(q, k, key_scale, weights, act_q, act_k, B, S1, S2, N1, D, sparse_mode, logits,
+                             ld, row_len, group_max, ld_g, stream);
 }
 
 namespace dsa {
 int topk_launch(const float* x, int64_t rows, int64_t cols, int64_t ld, const int32_t* row_len,
-                int32_t K, int32_t pad_invalid, int32_t* out_idx, float* out_val,
-                hipStream_t stream);
+                const float* gmax, int64_t ld_g, int32_t K, int32_t pad_invalid, int32_t* out_idx,
+                float* out_val, hipStream_t stream);
 }
 
+namespace {
+// Workspace of the full indexer: fp32 logits [rows, S2] | int32 row_len [rows] |
+// fp32 maxima of 16-key groups [rows, ceil(S2 / 16)], each part 256-byte aligned.
+struct IndexerWorkspace {
+  size_t rowlen_off, gmax_off, bytes;
+  int64_t ld_g;
+};
+
+IndexerWorkspace indexer_workspace(int64_t rows_in, int64_t S2_in) {
+  const size_t rows = (size_t)(rows_in < 0 ? 0 : rows_in);
+  const size_t S2 = (size_t)(S2_in < 0 ? 0 : S2_in);
+  auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
+  IndexerWorkspace w;
+  w.ld_g = (int64_t)((S2 + 15) / 16);
+  w.rowlen_off = up(rows * S2 * sizeof(float));
+  w.gmax_off = w.rowlen_off + up(rows * sizeof(int32_t));
+  w.bytes = w.gmax_off + rows * (size_t)w.ld_g * sizeof(float);
+  return w;
+}
+
+// The top-k reads the group maxima (and only the groups that can hold a top-K
+// element) when a row has at least 2 K groups; below that it streams the row.
+bool use_group_max(int64_t S2, int32_t K) { return (S2 + 15) / 16 >= 2 * (int64_t)K; }
+}  // namespace
+
 extern "C" size_t dsa_lightning_indexer_workspace_bytes(int64_t B, int64_t S1, int64_t S2) {
-  const size_t rows = (size_t)(B < 0 ? 0 : B) * (size_t)(S1 < 0 ? 0 : S1);
-  const size_t logits = rows * (size_t)(S2 < 0 ? 0 : S2) * sizeof(float);
-  return ((logits + 255) & ~size_t(255)) + rows * sizeof(int32_t);
+  return indexer_workspace((B < 0 ? 0 : B) * (S1 < 0 ? 0 : S1), S2).bytes;
 }
 
 extern "C" int dsa_lightning_indexer_fp8(const void* q, const void* k, const float* key_scale,
@@ -517,26 +605,27 @@ extern "C" int dsa_lightning_indexer_fp8(const void* q, const void* k, const flo
     return set_error(kWorkspaceTooSmall, "dsa_lightning_indexer_fp8: workspace of %zu bytes needed, %zu given",
                      need, workspace_bytes);
   if (indices == nullptr) return set_error(kInvalidArgument, "dsa_lightning_indexer_fp8: null indices");
+  const IndexerWorkspace wl = indexer_workspace(B * S1, S2);
   float* logits = static_cast<float*>(workspace);
-  const size_t logit_bytes = (size_t)B * S1 * S2 * sizeof(float);
-  int32_t* row_len = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + ((logit_bytes + 255) & ~size_t(255)));
+  int32_t* row_len = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + wl.rowlen_off);
+  float* gmax = use_group_max(S2, sparse_count) ? reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.gmax_off)
+                                                : nullptr;
   hipStream_t st = (hipStream_t)stream;
   if (S2 == 0)  // no keys: every row is all -1, the top-k kernel handles cols == 0
-    return topk_launch(logits, B * S1, 0, 0, nullptr, sparse_count, 1, indices, values, st);
-  int rc = dsa_indexer_logits_fp8(q, k, key_scale, weights, act_q, act_k, B, S1, S2, N1, D,
-                                  sparse_mode, logits, S2, row_len, stream);
+    return topk_launch(logits, B * S1, 0, 0, nullptr, nullptr, 0, sparse_count, 1, indices, values, st);
+  int rc = indexer_logits_impl(q, k, key_scale, weights, act_q, act_k, B, S1, S2, N1, D, sparse_mode, logits,
+                               S2, row_len, gmax, wl.ld_g, stream);
   if (rc != kOk) return rc;
-  return topk_launch(logits, B * S1, S2, S2, row_len, sparse_count, 1, indices, values, st);
+  return topk_launch(logits, B * S1, S2, S2, row_len, gmax, wl.ld_g, sparse_count, 1, indices, values, st);
 }
 
-extern "C" int dsa_indexer_logits_fp8_varlen(const void* q, const void* k, const float* key_scale,
-                                             const float* weights, const int32_t* seq_q,
-                                             int32_t seq_q_cumulative, const int32_t* seq_k,
-                                             int32_t seq_k_cumulative, const int32_t* block_table,
-                                             int32_t block_size, int32_t max_blocks, int64_t pool_rows,
-                                             int64_t B, int64_t S1, int64_t S2, int32_t N1, int32_t D,
-                                             int32_t sparse_mode, float* logits, int64_t ld,
-                                             int32_t* row_len, void* stream) {
+namespace {
+int indexer_logits_varlen_impl(const void* q, const void* k, const float* key_scale, const float* weights,
+                               const int32_t* seq_q, int32_t seq_q_cumulative, const int32_t* seq_k,
+                               int32_t seq_k_cumulative, const int32_t* block_table, int32_t block_size,
+                               int32_t max_blocks, int64_t pool_rows, int64_t B, int64_t S1, int64_t S2,
+                               int32_t N1, int32_t D, int32_t sparse_mode, float* logits, int64_t ld,
+                               int32_t* row_len, float* gmax, int64_t ld_g, void* stream) {
   using namespace dsa;
   if (N1 != kHeads || D != kDim)
     return set_error(kUnsupported,
@@ -566,12 +655,26 @@ extern "C" int dsa_indexer_logits_fp8_varlen(const void* q, const void* k, const
   const int32_t* cum_k = seq_k_cumulative ? seq_k : nullptr;
   return indexer_fp8_launch(static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(k), key_scale,
                             weights, act_q, act_k, cum_q, cum_k, block_table, block_size, max_blocks,
-                            pool_rows, (int)B, (int)S1, (int)S2, sparse_mode, logits, ld, row_len,
-                            (hipStream_t)stream);
+                            pool_rows, (int)B, (int)S1, (int)S2, sparse_mode, logits, ld, row_len, gmax,
+                            ld_g, (hipStream_t)stream);
+}
+}  // namespace
+
+extern "C" int dsa_indexer_logits_fp8_varlen(const void* q, const void* k, const float* key_scale,
+                                             const float* weights, const int32_t* seq_q,
+                                             int32_t seq_q_cumulative, const int32_t* seq_k,
+                                             int32_t seq_k_cumulative, const int32_t* block_table,
+                                             int32_t block_size, int32_t max_blocks, int64_t pool_rows,
+                                             int64_t B, int64_t S1, int64_t S2, int32_t N1, int32_t D,
+                                             int32_t sparse_mode, float* logits, int64_t ld,
+                                             int32_t* row_len, void* stream) {
+  return indexer_logits_varlen_impl(q, k, key_scale, weights, seq_q, seq_q_cumulative, seq_k, seq_k_cumulative,
+                                    block_table, block_size, max_blocks, pool_rows, B, S1, S2, N1, D,
+                                    sparse_mode, logits, ld, row_len, nullptr, 0, stream);
 }
 
 extern "C" size_t dsa_lightning_indexer_varlen_workspace_bytes(int64_t q_rows, int64_t S2) {
-  return dsa_lightning_indexer_workspace_bytes(1, q_rows, S2);
+  return indexer_workspace(q_rows, S2).bytes;
 }
 
 extern "C" int dsa_lightning_indexer_fp8_varlen(const void* q, const void* k, const float* key_scale,
@@ -598,16 +701,17 @@ extern "C" int dsa_lightning_indexer_fp8_varlen(const void* q, const void* k, co
                      "dsa_lightning_indexer_fp8_varlen: workspace of %zu bytes needed, %zu given", need,
                      workspace_bytes);
   if (indices == nullptr) return set_error(kInvalidArgument, "dsa_lightning_indexer_fp8_varlen: null indices");
+  const IndexerWorkspace wl = indexer_workspace(q_rows, S2);
   float* logits = static_cast<float*>(workspace);
-  const size_t logit_bytes = (size_t)q_rows * S2 * sizeof(float);
-  int32_t* row_len =
-      reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + ((logit_bytes + 255) & ~size_t(255)));
+  int32_t* row_len = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + wl.rowlen_off);
+  float* gmax = use_group_max(S2, sparse_count) ? reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.gmax_off)
+                                                : nullptr;
   hipStream_t st = (hipStream_t)stream;
   if (S2 == 0 || B == 0 || S1 == 0)  // no keys (or no rows to score): every row is all -1
-    return topk_launch(logits, q_rows, 0, 0, nullptr, sparse_count, 1, indices, values, st);
-  int rc = dsa_indexer_logits_fp8_varlen(q, k, key_scale, weights, seq_q, seq_q_cumulative, seq_k,
-                                         seq_k_cumulative, block_table, block_size, max_blocks, pool_rows,
-                                         B, S1, S2, N1, D, sparse_mode, logits, S2, row_len, stream);
+    return topk_launch(logits, q_rows, 0, 0, nullptr, nullptr, 0, sparse_count, 1, indices, values, st);
+  int rc = indexer_logits_varlen_impl(q, k, key_scale, weights, seq_q, seq_q_cumulative, seq_k, seq_k_cumulative,
+                                      block_table, block_size, max_blocks, pool_rows, B, S1, S2, N1, D,
+                                      sparse_mode, logits, S2, row_len, gmax, wl.ld_g, stream);
   if (rc != kOk) return rc;
-  return topk_launch(logits, q_rows, S2, S2, row_len, sparse_count, 1, indices, values, st);
+  return topk_launch(logits, q_rows, S2, S2, row_len, gmax, wl.ld_g, sparse_count, 1, indices, values, st);
 }

@@ -249,6 +249,8 @@ __device__ __forceinline__ void sort_desc(uint64_t* buf, uint64_t* xbuf) {
 struct TopkArgs {
   const float* x;          // [rows, ld]
   const int32_t* row_len;  // [rows] or null
+  const float* gmax;       // [rows, ld_g] upper bounds of 16-element group maxima, or null
+  int64_t ld_g;
   int32_t* out_idx;        // [rows, K]
   float* out_val;          // [rows, K] or null
   int64_t ld;
@@ -548,17 +550,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ITEMS 
       const int64_t want = (164ll * L + 64ll * (K + K / 4 + 64) - 1) / (64ll * (K + K / 4 + 64));
       int nb = want < 16 ? 16 : (want > kSampleBlocks ? kSampleBlocks : (int)want);
       if (nb > L / 256) nb = L / 256;
-      const int ns = nb * 64;
-      if (L >= 8 * K && nb >= 16) {
-        constexpr int kPer = kSampleBlocks * 64 / kThreads;
+      constexpr int kPer = kSampleBlocks * 64 / kThreads;
+      // Given the maxima of the row's 16-element groups (the indexer emits them),
+      // those replace the sample: the K-th largest group maximum is a lower bound
+      // of the K-th largest element, and only the groups reaching it are read.
+      const int ng = (L + 15) >> 4;
+      const bool use_g = ITEMS == 0 && a.gmax != nullptr && ng >= 2 * K && ng <= kPer * kThreads &&
+                         (reinterpret_cast<uintptr_t>(xr) & 15) == 0;
+      const int ns = use_g ? ng : nb * 64;
+      if (use_g || (L >= 8 * K && nb >= 16)) {
         uint32_t sv[kPer];
         uint32_t smin = 0xffffffffu, smax = 0u;
+        const float* grow = use_g ? a.gmax + row * a.ld_g : nullptr;
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
           const int i = tid + u * kThreads;
-          const int blk = i >> 6;
-          const int start = (int)(((int64_t)blk * L / nb) & ~63);
-          sv[u] = i < ns ? ordered_key(xr[start + (i & 63)]) : 0u;
+          if (use_g) {
+            sv[u] = i < ns ? ordered_key(grow[i]) : 0u;
+          } else {
+            const int blk = i >> 6;
+            const int start = (int)(((int64_t)blk * L / nb) & ~63);
+            sv[u] = i < ns ? ordered_key(xr[start + (i & 63)]) : 0u;
+          }
         }
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
@@ -567,8 +580,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ITEMS 
             smax = sv[u] > smax ? sv[u] : smax;
           }
         }
-        // rank of the threshold inside the sample: ~1.25 K + 64 expected above it
-        const uint32_t r = (uint32_t)(((int64_t)(K + K / 4 + 64) * ns + L - 1) / L);
+        // rank of the threshold inside the sample: ~1.25 K + 64 expected above
+        // it; among group maxima exactly K (at least K groups, hence at least K
+        // elements, reach T)
+        const uint32_t r = use_g ? (uint32_t)K : (uint32_t)(((int64_t)(K + K / 4 + 64) * ns + L - 1) / L);
         // histogram of the sample over buckets spread evenly across its own key
         // range (bin kBins - 1 - bucket: larger values in higher bins)
         clear_hist(*sh);
@@ -611,19 +626,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ITEMS 
             // x >= value(T) <=> ordered(x) >= T) and store (bits, index); the
             // composites are formed afterwards, for the candidates only
             const float Tf = key_value(T);
-            constexpr int kStep = 8 * kThreads;  // two float4 per thread per batch
-            const bool vec = (reinterpret_cast<uintptr_t>(xr) & 15) == 0;
-            const int L4 = vec ? (L & ~3) : 0;
-            const int wbase = 4 * (tid & ~63);  // this wave's first element in a batch
-            auto load = [=](dsa::f32x4& v0, dsa::f32x4& v1, int e) {
-              const dsa::f32x4 z = {0.f, 0.f, 0.f, 0.f};
-              v0 = e < L4 ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e)) : z;
-              v1 = e + 4 * kThreads < L4
-                       ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e + 4 * kThreads))
-                       : z;
-            };
-            auto consume = [&](const dsa::f32x4& v0, const dsa::f32x4& v1, int e) {
-              const bool ok0 = e < L4, ok1 = e + 4 * kThreads < L4;
+            // appends the hits among two float4 of elements e0.. and e1.. as
+            // (bits, index); ok0 / ok1: the whole float4 is inside the row
+            auto take8 = [&](const dsa::f32x4& v0, int e0, bool ok0, const dsa::f32x4& v1, int e1, bool ok1) {
               const bool h[8] = {ok0 && v0[0] >= Tf, ok0 && v0[1] >= Tf, ok0 && v0[2] >= Tf, ok0 && v0[3] >= Tf,
                                  ok1 && v1[0] >= Tf, ok1 && v1[1] >= Tf, ok1 && v1[2] >= Tf, ok1 && v1[3] >= Tf};
               uint64_t m[8];
@@ -643,7 +648,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ITEMS 
                     const uint32_t slot = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m[j] >> 32),
                                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)m[j], 0u));
                     const float x = j < 4 ? v0[j & 3] : v1[j & 3];
-                    const int ej = e + (j < 4 ? 0 : 4 * kThreads) + (j & 3);
+                    const int ej = (j < 4 ? e0 : e1) + (j & 3);
                     if (h[j] && slot < (uint32_t)kCandCap)
                       cand[slot] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)ej;
                     base += (uint32_t)__popcll(m[j]);
@@ -651,26 +656,101 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ITEMS 
                 }
               }
             };
-            dsa::f32x4 a0, a1, b0v, b1v;
-            if (wbase < L4) load(a0, a1, 4 * tid);
-            for (int c0 = 0; wbase + c0 < L4; c0 += 2 * kStep) {
-              const bool more1 = wbase + c0 + kStep < L4, more2 = wbase + c0 + 2 * kStep < L4;
-              if (more1) load(b0v, b1v, 4 * tid + c0 + kStep);
-              consume(a0, a1, 4 * tid + c0);
-              if (more2) load(a0, a1, 4 * tid + c0 + 2 * kStep);
-              if (more1) consume(b0v, b1v, 4 * tid + c0 + kStep);
-            }
-            // the scalar tail (and unaligned rows): one element per lane per call
-            for (int e0 = L4; e0 < L; e0 += kThreads) {
-              const int e = e0 + tid;
+            // one element per lane per call (row tails, unaligned rows)
+            auto take1 = [&](int e) {
               const float x = e < L ? xr[e] : 0.f;
               append([&](int) { return e < L && x >= Tf; },
                      [&](int) { return ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)e; }, IntC<1>{});
+            };
+            if (use_g) {
+              // list the groups whose maximum reaches T (in the sel area, which
+              // is free until the ordering), then read each listed group as four
+              // float4, two per thread in flight
+              uint32_t* glist = reinterpret_cast<uint32_t*>(sel);
+              constexpr uint32_t kGroupCap = 2u * kSel;
+              {
+                uint64_t m[kPer];
+                uint32_t tot = 0;
+#pragma unroll
+                for (int u = 0; u < kPer; ++u) {
+                  m[u] = __ballot(tid + u * kThreads < ns && sv[u] >= T);
+                  tot += (uint32_t)__popcll(m[u]);
+                }
+                if (tot != 0) {
+                  uint32_t base = 0;
+                  if (lane == 0) base = atomicAdd(&sh->cnt[0], tot);
+                  base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+                  for (int u = 0; u < kPer; ++u) {
+                    if (m[u] != 0) {
+                      const uint32_t slot = base + __builtin_amdgcn_mbcnt_hi(
+                                                       (uint32_t)(m[u] >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)m[u], 0u));
+                      if (tid + u * kThreads < ns && sv[u] >= T && slot < kGroupCap)
+                        glist[slot] = (uint32_t)(tid + u * kThreads);
+                      base += (uint32_t)__popcll(m[u]);
+                    }
+                  }
+                }
+              }
+              __syncthreads();
+              const uint32_t nl = sh->cnt[0];
+              if (nl <= kGroupCap) {
+                const int items = 4 * (int)nl;
+                const dsa::f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                for (int j0 = tid; j0 - tid < items; j0 += 2 * kThreads) {
+                  const int j1 = j0 + kThreads;
+                  const int e0 = j0 < items ? 16 * (int)glist[j0 >> 2] + 4 * (j0 & 3) : L;
+                  const int e1 = j1 < items ? 16 * (int)glist[j1 >> 2] + 4 * (j1 & 3) : L;
+                  const bool f0 = e0 + 4 <= L, f1 = e1 + 4 <= L;
+                  const dsa::f32x4 v0 = f0 ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e0)) : z;
+                  const dsa::f32x4 v1 = f1 ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e1)) : z;
+                  take8(v0, e0, f0, v1, e1, f1);
+                  // a group that runs past the row end (its last float4s)
+                  const bool p0 = e0 < L && !f0, p1 = e1 < L && !f1;
+                  if (__ballot(p0 || p1) != 0) {
+                    for (int q = 0; q < 4; ++q) {
+                      const int eq0 = p0 ? e0 + q : L, eq1 = p1 ? e1 + q : L;
+                      take1(eq0);
+                      take1(eq1);
+                    }
+                  }
+                }
+              } else if (tid == 0) {
+                sh->cnt[1] = (uint32_t)kCandCap + 1u;  // too many groups: the exact passes decide
+              }
+            } else {
+              constexpr int kStep = 8 * kThreads;  // two float4 per thread per batch
+              const bool vec = (reinterpret_cast<uintptr_t>(xr) & 15) == 0;
+              const int L4 = vec ? (L & ~3) : 0;
+              const int wbase = 4 * (tid & ~63);  // this wave's first element in a batch
+              auto load = [=](dsa::f32x4& v0, dsa::f32x4& v1, int e) {
+                const dsa::f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                v0 = e < L4 ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e)) : z;
+                v1 = e + 4 * kThreads < L4
+                         ? __builtin_nontemporal_load(reinterpret_cast<const dsa::f32x4*>(xr + e + 4 * kThreads))
+                         : z;
+              };
+              auto consume = [&](const dsa::f32x4& v0, const dsa::f32x4& v1, int e) {
+                take8(v0, e, e < L4, v1, e + 4 * kThreads, e + 4 * kThreads < L4);
+              };
+              dsa::f32x4 a0, a1, b0v, b1v;
+              if (wbase < L4) load(a0, a1, 4 * tid);
+              for (int c0 = 0; wbase + c0 < L4; c0 += 2 * kStep) {
+                const bool more1 = wbase + c0 + kStep < L4, more2 = wbase + c0 + 2 * kStep < L4;
+                if (more1) load(b0v, b1v, 4 * tid + c0 + kStep);
+                consume(a0, a1, 4 * tid + c0);
+                if (more2) load(a0, a1, 4 * tid + c0 + 2 * kStep);
+                if (more1) consume(b0v, b1v, 4 * tid + c0 + kStep);
+              }
+              // the scalar tail (and unaligned rows)
+              for (int e0 = L4; e0 < L; e0 += kThreads) take1(e0 + tid);
             }
           }
           __syncthreads();
           const uint32_t nc = sh->cnt[1];
           have_cand = nc >= (uint32_t)K && nc <= (uint32_t)kCandCap;
+          if (tid == 0) sh->cnt[0] = 0u;  // the group list's count (sel is empty)
           if constexpr (ITEMS == 0) {
             if (have_cand) {
               // form the composites, keep the largest key for the bucket map and
@@ -824,12 +904,14 @@ int launch_items(const TopkArgs& a, int64_t rows, hipStream_t stream) {
 namespace dsa {
 
 int topk_launch(const float* x, int64_t rows, int64_t cols, int64_t ld, const int32_t* row_len,
-                int32_t K, int32_t pad_invalid, int32_t* out_idx, float* out_val,
-                hipStream_t stream) {
+                const float* gmax, int64_t ld_g, int32_t K, int32_t pad_invalid, int32_t* out_idx,
+                float* out_val, hipStream_t stream) {
   if (rows == 0 || K == 0) return kOk;
   TopkArgs a;
   a.x = x;
   a.row_len = row_len;
+  a.gmax = gmax;
+  a.ld_g = ld_g;
   a.out_idx = out_idx;
   a.out_val = out_val;
   a.ld = ld;
@@ -855,6 +937,27 @@ extern "C" int dsa_topk_f32(const float* scores, int64_t rows, int64_t cols, int
                      (long long)cols);
   if (rows > 0 && k > 0 && (scores == nullptr || out_idx == nullptr))
     return set_error(kInvalidArgument, "dsa_topk_f32: null scores or out_idx");
-  return topk_launch(scores, rows, cols, ld, row_len, k, pad_invalid, out_idx, out_val,
+  return topk_launch(scores, rows, cols, ld, row_len, nullptr, 0, k, pad_invalid, out_idx, out_val,
+                     (hipStream_t)stream);
+}
+
+extern "C" int dsa_topk_f32_group_max(const float* scores, int64_t rows, int64_t cols, int64_t ld,
+                                      const int32_t* row_len, const float* group_max, int64_t ld_g,
+                                      int32_t k, int32_t pad_invalid, int32_t* out_idx, float* out_val,
+                                      void* stream) {
+  using namespace dsa;
+  if (group_max != nullptr && ld_g < (cols + 15) / 16)
+    return set_error(kInvalidArgument, "dsa_topk_f32_group_max: ld_g=%lld < ceil(cols / 16)", (long long)ld_g);
+  if (rows < 0 || cols < 0 || ld < cols || k < 0)
+    return set_error(kInvalidArgument, "dsa_topk_f32_group_max: bad sizes rows=%lld cols=%lld ld=%lld k=%d",
+                     (long long)rows, (long long)cols, (long long)ld, k);
+  if (k > 8192)
+    return set_error(kUnsupported, "dsa_topk_f32_group_max: k=%d exceeds the supported maximum 8192", k);
+  if (cols >= (int64_t)1 << 31 || rows >= (int64_t)1 << 31)
+    return set_error(kUnsupported, "dsa_topk_f32_group_max: rows=%lld cols=%lld exceed 2^31-1", (long long)rows,
+                     (long long)cols);
+  if (rows > 0 && k > 0 && (scores == nullptr || out_idx == nullptr))
+    return set_error(kInvalidArgument, "dsa_topk_f32_group_max: null scores or out_idx");
+  return topk_launch(scores, rows, cols, ld, row_len, group_max, ld_g, k, pad_invalid, out_idx, out_val,
                      (hipStream_t)stream);
 }

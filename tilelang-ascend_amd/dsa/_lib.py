@@ -20,8 +20,12 @@ SIGNATURES = {
     "dsa_clear_error": (None, []),
     "dsa_abi_version": (c_i32, []),
     "dsa_topk_f32": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "dsa_topk_f32_group_max": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp,
+                                       c_vp, c_vp]),
     "dsa_indexer_logits_fp8": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                                        c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp]),
+    "dsa_indexer_logits_fp8_group_max": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
+                                                 c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
     "dsa_lightning_indexer_workspace_bytes": (c_sz, [c_i64, c_i64, c_i64]),
     "dsa_lightning_indexer_fp8": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                                           c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_sz, c_vp]),

@@ -65,7 +65,8 @@ def _int32_vec(name: str, t: Optional[torch.Tensor], n: int, device) -> Optional
 # top-k selector
 # ---------------------------------------------------------------------------
 def topk_selector(x: torch.Tensor, top_k: int, *, row_len: Optional[torch.Tensor] = None,
-                  pad_invalid: bool = True, return_values: bool = False):
+                  pad_invalid: bool = True, return_values: bool = False,
+                  group_max: Optional[torch.Tensor] = None):
     """Row-wise top-k of fp32 ``x [B, N]`` -> int32 indices ``[B, top_k]``.
 
     Same output as the topk_selector example's reference ``torch.topk(x, k)[1]``
@@ -74,6 +75,9 @@ def topk_selector(x: torch.Tensor, top_k: int, *, row_len: Optional[torch.Tensor
     ascending index order (examples/deepseek_v4/lightning_indexer.py:318-320).
     With ``pad_invalid`` entries whose value is <= -1e30 (masked) become -1, and
     rows shorter than ``top_k`` (``row_len``) are padded with -1 (:321-325).
+    ``group_max [B, ceil(N / 16)]`` fp32 (optional): upper bounds of the maxima of
+    each row's 16-element groups, as the lightning indexer emits them; long rows
+    then read only the groups that can hold a selected element (same result).
     """
     if x.dim() != 2:
         raise ValueError(f"x must be 2-D [B, N], got shape {tuple(x.shape)}")
@@ -87,8 +91,18 @@ def topk_selector(x: torch.Tensor, top_k: int, *, row_len: Optional[torch.Tensor
     rl = _int32_vec("row_len", row_len, B, dev)
     idx = torch.empty((B, top_k), dtype=torch.int32, device=dev)
     val = torch.empty((B, top_k), dtype=torch.float32, device=dev) if return_values else None
-    check(lib().dsa_topk_f32(_ptr(x), B, N, N, _ptr(rl), top_k, int(bool(pad_invalid)), _ptr(idx),
-                             _ptr(val), _stream(dev)), "dsa_topk_f32")
+    if group_max is None:
+        check(lib().dsa_topk_f32(_ptr(x), B, N, N, _ptr(rl), top_k, int(bool(pad_invalid)), _ptr(idx),
+                                 _ptr(val), _stream(dev)), "dsa_topk_f32")
+    else:
+        ng = (N + 15) // 16
+        if group_max.dtype != torch.float32 or tuple(group_max.shape) != (B, ng):
+            raise ValueError(f"group_max must be float32 [{B}, {ng}], got {group_max.dtype} {tuple(group_max.shape)}")
+        _require_gpu(x, group_max)
+        _require_contiguous("group_max", group_max)
+        check(lib().dsa_topk_f32_group_max(_ptr(x), B, N, N, _ptr(rl), _ptr(group_max), ng, top_k,
+                                           int(bool(pad_invalid)), _ptr(idx), _ptr(val), _stream(dev)),
+              "dsa_topk_f32_group_max")
     return (idx, val) if return_values else idx
 
 
