@@ -258,11 +258,70 @@ def target_configs(L, steps: int) -> dict:
     uq = _time_launches(qq, steps)
     kbytes = kb.numel() * 3 + ks.numel() * 4
     qbytes = qb.numel() * 3 + wq.numel() * 8
+    del kb, k8, ks, qb, wq, q8, wo
+    torch.cuda.empty_cache()
+    res["flash_mla_v4"] = flash_mla_v4_configs(L, steps)
     res["fp8_producers"] = {"key_cache_128k_us": round(uk, 2),
                             "key_cache_frac_of_hbm": round(kbytes / uk / 1e3 / PEAK_HBM_GBS, 4),
                             "query_4096_us": round(uq, 2),
                             "query_frac_of_hbm": round(qbytes / uq / 1e3 / PEAK_HBM_GBS, 4),
                             "algorithmic_bytes": {"key_cache": kbytes, "query": qbytes}}
+    return res
+
+
+def flash_mla_v4_configs(L, steps: int) -> dict:
+    """DeepSeek-V4 sparse flash MLA at the reference's benchmark shapes
+    (examples/deepseek_v4/sparse_flash_mla/bench_mark.md: B=1, N1=64, D=512, block 128,
+    window 127, K=512, cmp_ratio 4 (swa / csa) or 128 (hca); prefill S = 8192, decode
+    one row against 8193 keys).  FLOP = 4 * N1 * D per attended (row, key)."""
+    import torch
+
+    from dsa import inputs
+
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream(dev).cuda_stream
+    res = {}
+    for name, scen, ratio in (("swa", 1, 4), ("hca", 2, 128), ("csa", 3, 4)):
+        for mode, S, kv in (("prefill", 8192, 8192), ("decode", 1, 8193)):
+            c = inputs.flash_mla_v4(scenario=scen, S1=S, seqused_kv=[kv], cmp_ratio=ratio, K=512, seed=11)
+            T = S
+            q = c["q"].to(dev)
+            ori, obt = c["ori_kv"].to(dev), c["ori_block_table"].to(dev)
+            cmp = c["cmp_kv"].to(dev) if c["cmp_kv"] is not None else None
+            cbt = c["cmp_block_table"].to(dev) if cmp is not None else None
+            ci = c["cmp_sparse_indices"].view(T, -1).to(dev) if c["cmp_sparse_indices"] is not None else None
+            n_cmp = 512 if scen == 3 else (kv // ratio if scen == 2 else 0)
+            qp = torch.zeros((1,), dtype=torch.int32, device=dev)
+            aq = torch.full((1,), S, dtype=torch.int32, device=dev)
+            kvl = torch.full((1,), kv, dtype=torch.int32, device=dev)
+            sk = c["sinks"].to(dev)
+            out = torch.empty((T, 64, 512), dtype=torch.bfloat16, device=dev)
+            lse = torch.empty((T, 64), dtype=torch.float32, device=dev)
+            wsb = L.dsa_sparse_flash_mla_workspace_bytes(T, 64, 127, n_cmp)
+            ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+
+            def run():
+                rc = L.dsa_sparse_flash_mla(
+                    q.data_ptr(), T, 64, 512, qp.data_ptr(), aq.data_ptr(), kvl.data_ptr(), 1, ori.data_ptr(),
+                    ori.shape[0], ori.shape[1], obt.data_ptr(), obt.shape[1], cmp.data_ptr() if cmp is not None else None,
+                    cmp.shape[0] if cmp is not None else 0, cmp.shape[1] if cmp is not None else 0,
+                    cbt.data_ptr() if cbt is not None else None, cbt.shape[1] if cbt is not None else 0,
+                    ci.data_ptr() if ci is not None else None, 512 if scen == 3 else 0, n_cmp, ratio,
+                    sk.data_ptr(), 0.04419417, 127, out.data_ptr(), lse.data_ptr(), ws.data_ptr(), wsb, st)
+                if rc != 0:
+                    raise RuntimeError(f"flash_mla_v4 {name}: {L.dsa_last_error().decode()}")
+
+            us = _time_launches(run, max(2, steps // 2))
+            keys = 0
+            for s_ in range(S):
+                sg = kv - S + s_
+                keys += min(sg + 1, 128)
+                thr = (sg + 1) // ratio
+                keys += 0 if scen == 1 else (thr if scen == 2 else min(512, thr))
+            fl = 4.0 * 64 * 512 * keys
+            res[f"{name}_{mode}"] = {"us": round(us, 2), "tflops": round(fl / us / 1e6, 2)}
+            del c, q, ori, obt, cmp, cbt, ci, out, lse, ws
+    torch.cuda.empty_cache()
     return res
 
 

@@ -198,6 +198,36 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices,
                        void* stream);
 
 /*
+ * DeepSeek-V4 sparse flash MLA: sliding window over the original KV plus the
+ * compressed KV, with sinks.  Replaces the call behind sparse_flash_mla
+ * (examples/deepseek_v4/sparse_flash_mla/sparse_flash_mla_api.py:94-253; kernel
+ * sparse_flash_mla_kernel.py:1099-2166) with the golden's semantics
+ * (sparse_flash_mla_golden.py:56-153).
+ *   q [T, N1, 512] bf16; query row s of batch b is row q_prefix[b] + s for
+ *     s < act_q_lens[b] (TND: q_prefix = cu_seqlens_q[:-1]; BSND: b * S);
+ *     its position is seqused_kv[b] - act_q_lens[b] + s.
+ *   ori_kv [ori_blocks, ori_block_size, 1, 512] bf16 + ori_block_table [B, ori_table_len]:
+ *     the window of ori_win_left + 1 positions ending at the row's position.
+ *   cmp_kv [cmp_blocks, cmp_block_size, 1, 512] + cmp_block_table, or NULL (window only):
+ *     with cmp_sparse_indices [T, topk_cmp] int32 ("csa", n_cmp = topk_cmp) the
+ *     listed compressed positions below floor((position + 1) / cmp_ratio), read
+ *     up to the first -1; without ("hca") all compressed positions below it,
+ *     n_cmp >= the largest such count (max(seqused_kv) / cmp_ratio).
+ *   sinks [N1] fp32; K = V; out [T, N1, 512] bf16, lse [T, N1] fp32 (natural log)
+ *   or NULL.  Rows outside every batch get out = 0.
+ * workspace: dsa_sparse_flash_mla_workspace_bytes(T, N1, ori_win_left, n_cmp).
+ */
+size_t dsa_sparse_flash_mla_workspace_bytes(int64_t T, int32_t N1, int32_t ori_win_left, int32_t n_cmp);
+int dsa_sparse_flash_mla(const void* q, int64_t T, int32_t N1, int32_t D, const int32_t* q_prefix,
+                         const int32_t* act_q_lens, const int32_t* seqused_kv, int64_t B, const void* ori_kv,
+                         int64_t ori_blocks, int32_t ori_block_size, const int32_t* ori_block_table,
+                         int32_t ori_table_len, const void* cmp_kv, int64_t cmp_blocks, int32_t cmp_block_size,
+                         const int32_t* cmp_block_table, int32_t cmp_table_len,
+                         const int32_t* cmp_sparse_indices, int32_t topk_cmp, int32_t n_cmp, int32_t cmp_ratio,
+                         const float* sinks, float softmax_scale, int32_t ori_win_left, void* out, float* lse,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Row quantisation (the step before the indexer).  x is bf16 [rows, cols],
  * cols a multiple of 8, x 16-byte and y 8-byte aligned; one scale per row.
  *

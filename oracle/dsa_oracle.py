@@ -391,6 +391,95 @@ def lse_combine(outs: Sequence[torch.Tensor], lses: Sequence[torch.Tensor]):
 
 
 # ---------------------------------------------------------------------------
+# DeepSeek-V4 sparse flash MLA (window over the original KV + compressed KV)
+# ---------------------------------------------------------------------------
+def v4_compressed_positions(cmp_sparse_indices: Optional[torch.Tensor], b: int, s: int, act_kv: int, act_q: int,
+                            cmp_ratio: int, K: Optional[int] = None) -> list:
+    """Compressed positions query row ``s`` of batch ``b`` attends to
+    (sparse_flash_mla_golden.py:16-53 with sparse_block_size 1, and the dense
+    branch :120-122): threshold ``t = floor((act_kv - act_q + s + 1) / cmp_ratio)``;
+    without a list all of ``0 .. t - 1``; with one, its first ``min(K, t)`` entries
+    up to the first -1, each kept when ``< t`` and ``< floor(act_kv / cmp_ratio)``."""
+    thr = (act_kv - act_q + s + 1) // cmp_ratio
+    if cmp_sparse_indices is None:
+        return list(range(max(thr, 0)))
+    lst = cmp_sparse_indices[b, s].reshape(-1).tolist()
+    K = len(lst) if K is None else K
+    cmp_act = act_kv // cmp_ratio
+    pos = []
+    for i in range(min(K, max(thr, 0))):
+        e = lst[i]
+        if e == -1:
+            break
+        if 0 <= e < thr and e < cmp_act:
+            pos.append(e)
+    return pos
+
+
+def sparse_flash_mla_v4(q_bnsd: torch.Tensor, ori_k_bnsd: torch.Tensor, sinks: torch.Tensor, *,
+                        act_q_lens: Sequence[int], act_kv_lens: Sequence[int], softmax_scale: float,
+                        cmp_k_bnsd: Optional[torch.Tensor] = None,
+                        cmp_sparse_indices: Optional[torch.Tensor] = None, cmp_ratio: Optional[int] = None,
+                        ori_win_left: int = 127, s2_tile: int = 512):
+    """DeepSeek-V4 sparse flash MLA, the golden's loop restated
+    (sparse_flash_mla_golden.py:56-153): per query row, the window
+    ``[max(sg - ori_win_left, 0), sg]`` of the original keys (``sg = act_kv - act_q +
+    s``) then the compressed keys of :func:`v4_compressed_positions`, in tiles of
+    ``s2_tile`` with a running maximum that starts at the sink (sum starts at 1),
+    probabilities rounded to q's dtype before the P.V product; K = V.
+    q ``[B, N1, S, D]``, keys ``[B, 1, S_kv, D]``, sparse indices ``[B, S, 1, K]``.
+    Returns ``(out [B, N1, S, D] in q's dtype, lse [B, N1, S] fp32)``; rows past
+    ``act_q`` stay zero."""
+    B, N1, S, D = q_bnsd.shape
+    dtype = q_bnsd.dtype
+    out = torch.zeros_like(q_bnsd)
+    lse = torch.zeros((B, N1, S), dtype=torch.float32)
+    sink = sinks.to(torch.float32)
+    for b in range(B):
+        aq, akv = int(act_q_lens[b]), int(act_kv_lens[b])
+        for s in range(aq):
+            sg = akv - aq + s
+            q = q_bnsd[b, :, s, :].to(torch.float32)
+            keys = [ori_k_bnsd[b, 0, max(sg - ori_win_left, 0):sg + 1, :].to(torch.float32)]
+            if cmp_k_bnsd is not None:
+                pos = v4_compressed_positions(cmp_sparse_indices, b, s, akv, aq, cmp_ratio)
+                keys.append(cmp_k_bnsd[b, 0, pos, :].to(torch.float32))
+            m = sink.clone()
+            l = torch.ones(N1, dtype=torch.float32)
+            acc = torch.zeros((N1, D), dtype=torch.float32)
+            for kk in keys:
+                for t0 in range(0, kk.shape[0], s2_tile):
+                    kt = kk[t0:t0 + s2_tile]
+                    sc = (q @ kt.t()) * softmax_scale
+                    m_new = torch.maximum(m, sc.amax(dim=1))
+                    alpha = torch.exp(m - m_new)
+                    p = torch.exp(sc - m_new.unsqueeze(1))
+                    l = alpha * l + p.sum(dim=1)
+                    acc = acc * alpha.unsqueeze(1) + p.to(dtype).to(torch.float32) @ kt
+                    m = m_new
+            out[b, :, s, :] = (acc / l.unsqueeze(1)).to(dtype)
+            lse[b, :, s] = m + torch.log(l)
+    return out, lse
+
+
+def unpack_pages(pool: torch.Tensor, block_table: torch.Tensor, length: int) -> torch.Tensor:
+    """Page pool ``[blocks, bs, N2, D]`` + table ``[B, max_blocks]`` -> ``[B, N2, length, D]``
+    (sparse_flash_mla_golden.py:175-198; missing pages stay zero)."""
+    nb, bs, N2, D = pool.shape
+    B = block_table.shape[0]
+    out = pool.new_zeros((B, N2, length, D))
+    for b in range(B):
+        for i in range(block_table.shape[1]):
+            page = int(block_table[b, i])
+            lo = i * bs
+            if page < 0 or lo >= length:
+                continue
+            hi = min(lo + bs, length)
+            out[b, :, lo:hi, :] = pool[page, :hi - lo].permute(1, 0, 2)
+    return out
+
+
+# ---------------------------------------------------------------------------
 # row quantisation (the producer of the indexer's fp8 operands; int8 act quant)
 # ---------------------------------------------------------------------------
 FP8_MAX = 448.0
@@ -472,6 +561,9 @@ PINNED_BY = {
                    "invariance; LSE == logsumexp (tests/test_oracle_mla.py)",
     "sparse_mla_fwd_dense": "agreement with the gather form and brute force",
     "lse_combine": "split a row's index set in two, combine == unsplit result",
+    "sparse_flash_mla_v4": "the gather formulation on the same key sets (independent code), "
+                   "closed forms (no key: out 0 and lse = sink; one key: out = v e^s / (e^s + e^sink)), "
+                   "compressed-position rules against hand-worked lists (tests/test_oracle_mla.py)",
     "act_quant_int8/pow2_ceil": "the golden's torch formula (2**ceil(log2)) on random rows, "
                    "the reference test's tolerance (act_quant.py:162-163), max |y| = 127 at the "
                    "row maximum, |x - y s| <= s / 2, half-to-even ties on constructed rows, "

@@ -4,6 +4,7 @@
 closed forms and invariants."""
 import math
 
+import pytest
 import torch
 
 from oracle.dsa_oracle import lse_combine, pa_to_contiguous, sparse_mla_fwd_dense, sparse_mla_fwd_gather
@@ -130,3 +131,93 @@ def test_bf16_probability_rounding_stays_close():
     o1, _ = sparse_mla_fwd_gather(q, kv, idx, None, is_causal=False)
     o2, _ = sparse_mla_fwd_gather(q, kv, idx, None, is_causal=False, p_dtype=torch.bfloat16)
     assert torch.allclose(o1, o2, rtol=2e-2, atol=2e-2)
+
+
+# ---------------------------------------------------------------- DeepSeek-V4 sparse flash MLA
+from oracle.dsa_oracle import sparse_flash_mla_v4, unpack_pages, v4_compressed_positions  # noqa: E402
+
+
+def test_v4_compressed_positions_hand_worked():
+    idx = torch.tensor([[[5, 0, 9, 2, -1, 1]]], dtype=torch.int32).view(1, 1, 1, 6)
+    # act_kv 40, act_q 1, s 0: t = (40 - 1 + 0 + 1) // 4 = 10; the first min(6, 10) entries up to the -1
+    assert v4_compressed_positions(idx.view(1, 1, 6), 0, 0, 40, 1, 4) == [5, 0, 9, 2]
+    # t = (12 - 1 + 0 + 1) // 4 = 3: only the first min(K, t) = 3 entries are read
+    # (5, 0, 9), and of those only 0 lies below t
+    assert v4_compressed_positions(idx.view(1, 1, 6), 0, 0, 12, 1, 4) == [0]
+    # t = 5 reads 5, 0, 9, 2, -1: 0 and 2 (5 is not < 5)
+    assert v4_compressed_positions(idx.view(1, 1, 6), 0, 0, 20, 1, 4) == [0, 2]
+    # the -1 ends the list even when later entries would be in range
+    assert v4_compressed_positions(idx.view(1, 1, 6), 0, 0, 400, 1, 4) == [5, 0, 9, 2]
+    # dense (no list): all positions below t
+    assert v4_compressed_positions(None, 0, 0, 12, 1, 4) == [0, 1, 2]
+    assert v4_compressed_positions(None, 0, 0, 2, 4, 4) == []
+
+
+def _v4_small(seed, scenario):
+    g = torch.Generator().manual_seed(seed)
+    B, N1, D, win = 2, 4, 32, 6
+    act_q, act_kv = [5, 3], [17, 9]
+    S = max(act_q)
+    q = torch.randn((B, N1, S, D), generator=g).to(torch.bfloat16)
+    ori = torch.randn((B, 1, max(act_kv), D), generator=g).to(torch.bfloat16)
+    cmp = torch.randn((B, 1, max(act_kv) // 2, D), generator=g).to(torch.bfloat16) if scenario >= 2 else None
+    lists = None
+    if scenario == 3:
+        lists = torch.randint(0, 8, (B, S, 1, 5), generator=g, dtype=torch.int32)
+        lists[0, 1, 0, 3] = -1
+    sinks = torch.randn(N1, generator=g)
+    return dict(q=q, ori=ori, cmp=cmp, lists=lists, sinks=sinks, act_q=act_q, act_kv=act_kv, win=win, ratio=2,
+                scale=D ** -0.5)
+
+
+@pytest.mark.parametrize("scenario", [1, 2, 3])
+def test_v4_agrees_with_gather_formulation(scenario):
+    c = _v4_small(30 + scenario, scenario)
+    out, lse = sparse_flash_mla_v4(c["q"], c["ori"], c["sinks"], act_q_lens=c["act_q"], act_kv_lens=c["act_kv"],
+                                   softmax_scale=c["scale"], cmp_k_bnsd=c["cmp"], cmp_sparse_indices=c["lists"],
+                                   cmp_ratio=c["ratio"], ori_win_left=c["win"] - 1)
+    B, N1, S, D = c["q"].shape
+    n_ori = c["ori"].shape[2]
+    for b in range(B):
+        keys = c["ori"][b, 0] if c["cmp"] is None else torch.cat([c["ori"][b, 0], c["cmp"][b, 0]])
+        for s in range(c["act_q"][b]):
+            sg = c["act_kv"][b] - c["act_q"][b] + s
+            sel = list(range(max(sg - c["win"] + 1, 0), sg + 1))
+            if c["cmp"] is not None:
+                sel += [n_ori + p for p in v4_compressed_positions(c["lists"], b, s, c["act_kv"][b], c["act_q"][b],
+                                                                   c["ratio"])]
+            idx = torch.full((1, 1, 1, 32), -1, dtype=torch.int32)
+            idx[0, 0, 0, :len(sel)] = torch.tensor(sel, dtype=torch.int32)
+            ro, rl = sparse_mla_fwd_gather(c["q"][b, :, s].unsqueeze(0).unsqueeze(0), keys.view(1, -1, 1, D), idx,
+                                           c["scale"], d_v=D, attn_sink=c["sinks"], p_dtype=torch.bfloat16)
+            torch.testing.assert_close(out[b, :, s].float(), ro[0, 0], rtol=2e-2, atol=2e-2)
+            torch.testing.assert_close(lse[b, :, s], rl[0, 0], rtol=1e-5, atol=1e-5)
+
+
+def test_v4_closed_forms():
+    # a row before any key (act_kv < act_q): out 0 and lse = sink; a row seeing one
+    # key k with score x: out = k e^x / (e^x + e^sink), lse = ln(e^x + e^sink)
+    g = torch.Generator().manual_seed(3)
+    N1, D = 2, 16
+    q = torch.randn((1, N1, 3, D), generator=g).to(torch.bfloat16)
+    ori = torch.randn((1, 1, 1, D), generator=g).to(torch.bfloat16)
+    sinks = torch.tensor([0.3, -2.0])
+    out, lse = sparse_flash_mla_v4(q, ori, sinks, act_q_lens=[3], act_kv_lens=[1], softmax_scale=0.5,
+                                   ori_win_left=0)
+    # rows 0, 1 sit before the cache (positions -2, -1); row 2 sees key 0 only
+    assert torch.equal(out[0, :, :2].float(), torch.zeros(N1, 2, D))
+    torch.testing.assert_close(lse[0, :, 0], sinks)
+    x = (q[0, :, 2].float() @ ori[0, 0, 0].float()) * 0.5
+    w = torch.exp(x) / (torch.exp(x) + torch.exp(sinks))
+    torch.testing.assert_close(out[0, :, 2].float(), (w.unsqueeze(1) * ori[0, 0, 0].float()), rtol=1e-2, atol=1e-2)
+    torch.testing.assert_close(lse[0, :, 2], torch.logaddexp(x, sinks), rtol=1e-5, atol=1e-5)
+
+
+def test_unpack_pages_roundtrip():
+    g = torch.Generator().manual_seed(4)
+    pool = torch.randn((5, 4, 1, 3), generator=g)
+    bt = torch.tensor([[3, 0, -1], [1, 4, 2]], dtype=torch.int32)
+    u = unpack_pages(pool, bt, 10)
+    assert torch.equal(u[0, 0, 0:4], pool[3, :, 0]) and torch.equal(u[0, 0, 4:8], pool[0, :, 0])
+    assert torch.equal(u[0, 0, 8:10], torch.zeros(2, 3))
+    assert torch.equal(u[1, 0, 8:10], pool[2, :2, 0])

@@ -34,6 +34,7 @@
 // more than 2^8.  With more than one split the workgroups write normalised
 // partial outputs plus their LSE, and a combine kernel merges them.
 #include "dsa_common.h"
+#include "mla_run.h"
 
 namespace {
 
@@ -63,6 +64,11 @@ struct MlaParams {
   float* part_lse;              // [T, nsplit, H]
   int64_t skv;                  // keys per batch row (non-paged) or max_blocks * bs
   int64_t pool_rows;            // rows in the page pool (paged)
+  const uint16_t* kv2;          // second row pool (direct rows with the kRowTag2 bit) or null
+  int64_t pool_rows2;           // rows in the second pool
+  int direct;                   // indices are physical rows (kRowTag2: row of kv2), already resolved
+  int v4_on;                    // key sets generated from v4 (no index list)
+  dsa::V4Keys v4;
   int B, S, H, topk;
   int block_size, max_blocks;
   int nsplit, keys_per_split, nhg;
@@ -138,13 +144,36 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
   }
 
   // ---- resolve this split's indices to physical rows (-1 = skip) ----
-  {
+  if (p.v4_on) {
+    __shared__ int v4_sh[2];  // batch of this row, first -1 of its compressed list
+    if (tid == 0) {
+      v4_sh[0] = dsa::v4_batch(p.v4, token);
+      v4_sh[1] = p.v4.K;
+    }
+    __syncthreads();
+    const int vb = v4_sh[0];
+    if (vb >= 0 && p.v4.scenario == 3) {
+      const int32_t* ci = p.v4.cmp_idx + token * p.v4.K;
+      for (int j = tid; j < p.v4.K; j += NT)
+        if (ci[j] == -1) atomicMin(&v4_sh[1], j);
+      __syncthreads();
+    }
+    const int stop = v4_sh[1];
+    for (int j = tid; j < nkeys; j += NT) rows[j] = vb >= 0 ? dsa::v4_row(p.v4, token, vb, kbeg + j, stop) : -1;
+  } else {
     const int kvl = p.kv_len ? p.kv_len[b] : (int)(p.skv < 0x7fffffff ? p.skv : 0x7fffffff);
     const int qs = p.q_start ? p.q_start[b] : kvl - p.S;
     const int32_t* ip = p.indices + token * p.topk + kbeg;
     for (int j = tid; j < nkeys; j += NT) {
       const int idx = ip[j];
       int32_t row = -1;
+      if (p.direct) {
+        // resolved rows: bit 30 selects the second pool
+        const int r = idx & ~dsa::kRowTag2;
+        if (idx >= 0 && (int64_t)r < ((idx & dsa::kRowTag2) ? p.pool_rows2 : p.pool_rows)) row = idx;
+        rows[j] = row;
+        continue;
+      }
       bool ok = idx >= 0 && idx < kvl && (int64_t)idx < p.skv;
       if (ok && p.causal) ok = idx <= qs + s;
       if (ok) {
@@ -174,7 +203,10 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
     unsigned char* sb = smem + (step % kStages) * STAGE;
     const int kk = step * kKT + gkey;
     const int32_t rr = kk < nkeys ? rows[kk] : -1;
-    const uint16_t* src = (rr >= 0 ? p.kv + (int64_t)rr * DQK : g_zero_row) + 8 * gch0;
+    const uint16_t* src = (rr >= 0 ? ((rr & dsa::kRowTag2) ? p.kv2 + (int64_t)(rr & ~dsa::kRowTag2) * DQK
+                                                           : p.kv + (int64_t)rr * DQK)
+                                   : g_zero_row) +
+                          8 * gch0;
 #pragma unroll
     for (int i = 0; i < LOADS_HI; ++i) {
       if (i < LOADS_LO || many)
@@ -434,22 +466,111 @@ int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
 
 int choose_splits(int64_t tokens, int nhg, int topk) {
   // split the index list until the 256 CUs are covered, keeping >= 256 keys per
-  // split (more splits cost more fp32 partials than the extra CUs return)
+  // split (more splits cost more fp32 partials than the extra CUs return); a
+  // handful of rows (single-token decode) is latency bound instead, and splits
+  // down to 128 keys (below that the combine costs more than it saves)
+  const int min_keys = tokens * nhg >= 16 ? 256 : 128;
   int ns = 1;
-  while (tokens * nhg * ns < 256 && (topk + 2 * ns - 1) / (2 * ns) >= 256) ns *= 2;
+  while (tokens * nhg * ns < 256 && (topk + 2 * ns - 1) / (2 * ns) >= min_keys) ns *= 2;
   while ((topk + ns - 1) / ns > kMaxKeysPerSplit) ++ns;
   return ns;
 }
 
 }  // namespace
 
-extern "C" size_t dsa_sparse_mla_workspace_bytes(int64_t B, int64_t S, int32_t H, int32_t topk,
-                                                 int32_t num_splits) {
-  const int64_t T = B * S;
+namespace dsa {
+
+size_t sparse_mla_split_bytes(int64_t T, int32_t H, int32_t topk, int32_t num_splits) {
   const int nhg = (H + kHeadsPerGroup - 1) / kHeadsPerGroup;
   const int ns = num_splits > 0 ? num_splits : choose_splits(T, nhg, topk);
   if (ns <= 1) return 0;
   return (size_t)T * ns * H * (kDV + 1) * sizeof(float);
+}
+
+int sparse_mla_run(const MlaRun& r, const char* what) {
+  if (r.d_v != kDV) return set_error(kUnsupported, "%s: d_v must be 512 (got %d)", what, r.d_v);
+  if (r.d_qk != 576 && r.d_qk != 512)
+    return set_error(kUnsupported, "%s: d_qk must be 576 or 512 (got %d)", what, r.d_qk);
+  if (r.B < 0 || r.S < 0 || r.H <= 0 || r.topk < 0 || r.skv < 0)
+    return set_error(kInvalidArgument, "%s: bad sizes", what);
+  if (!(r.sm_scale > 0.f) || r.sm_scale == __builtin_inff())
+    return set_error(kInvalidArgument, "%s: sm_scale must be positive and finite", what);
+  if (r.block_table != nullptr && (r.block_size <= 0 || r.max_blocks <= 0))
+    return set_error(kInvalidArgument, "%s: paged KV needs block_size > 0 and max_blocks > 0", what);
+  const int64_t T = r.B * r.S;
+  if (T == 0) return kOk;
+  if (r.q == nullptr || r.kv == nullptr || (r.indices == nullptr && r.v4 == nullptr) || r.out == nullptr)
+    return set_error(kInvalidArgument, "%s: null pointer", what);
+  if (r.direct) {
+    if (r.skv > kRowTag2 || r.pool_rows2 > kRowTag2 || (r.pool_rows2 > 0 && r.kv2 == nullptr))
+      return set_error(kUnsupported, "%s: resolved rows need pools of at most 2^30 rows", what);
+  } else if ((r.block_table ? r.skv : r.B * r.skv) >= ((int64_t)1 << 31)) {
+    return set_error(kUnsupported, "%s: more than 2^31 - 1 KV rows", what);
+  }
+
+  MlaParams p;
+  p.q = static_cast<const uint16_t*>(r.q);
+  p.kv = static_cast<const uint16_t*>(r.kv);
+  p.indices = r.indices;
+  p.block_table = r.block_table;
+  p.kv_len = r.kv_len;
+  p.q_start = r.q_start;
+  p.sink = r.attn_sink;
+  p.out = static_cast<uint16_t*>(r.out);
+  p.lse = r.lse;
+  p.skv = r.block_table ? (int64_t)r.max_blocks * r.block_size : r.skv;
+  p.pool_rows = r.skv;
+  p.kv2 = static_cast<const uint16_t*>(r.kv2);
+  p.pool_rows2 = r.pool_rows2;
+  p.direct = r.direct;
+  p.v4_on = r.v4 != nullptr;
+  if (r.v4 != nullptr) p.v4 = *r.v4;
+  p.B = (int)r.B;
+  p.S = (int)r.S;
+  p.H = r.H;
+  p.topk = r.topk;
+  p.block_size = r.block_size;
+  p.max_blocks = r.max_blocks;
+  p.scale_log2 = r.sm_scale * kLog2e;
+  p.causal = r.is_causal;
+
+  p.nhg = (r.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  int ns = r.num_splits > 0 ? r.num_splits : choose_splits(T, p.nhg, r.topk);
+  if (r.topk == 0) ns = 1;
+  const int kps = r.topk > 0 ? (r.topk + ns - 1) / ns : 0;
+  if (kps > kMaxKeysPerSplit)
+    return set_error(kInvalidArgument, "%s: %d keys per split exceeds %d; raise num_splits", what, kps,
+                     kMaxKeysPerSplit);
+  p.nsplit = ns;
+  p.keys_per_split = kps;
+  if (ns > 1) {
+    const size_t need = (size_t)T * ns * r.H * (kDV + 1) * sizeof(float);
+    if (r.workspace == nullptr || r.workspace_bytes < need)
+      return set_error(kWorkspaceTooSmall, "%s: workspace of %zu bytes needed, %zu given", what, need,
+                       r.workspace_bytes);
+    p.part_o = static_cast<float*>(r.workspace);
+    p.part_lse = p.part_o + (size_t)T * ns * r.H * kDV;
+  } else {
+    p.part_o = nullptr;
+    p.part_lse = nullptr;
+  }
+  const int64_t units = T * ns;
+  const int64_t nblocks = ((units + kNumXcd - 1) / kNumXcd) * kNumXcd * p.nhg;
+  if (nblocks > 0x7fffffff) return set_error(kUnsupported, "%s: grid too large", what);
+  hipStream_t st = (hipStream_t)r.stream;
+  const int rc = r.d_qk == 576 ? launch_mla<576>(p, nblocks, st) : launch_mla<512>(p, nblocks, st);
+  if (rc != kOk || ns == 1) return rc;
+  const int64_t rows = T * r.H;
+  hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, st,
+                     p.part_o, p.part_lse, rows, r.H, ns, p.out, r.lse);
+  return check_launch("dsa_sparse_mla_fwd(combine)");
+}
+
+}  // namespace dsa
+
+extern "C" size_t dsa_sparse_mla_workspace_bytes(int64_t B, int64_t S, int32_t H, int32_t topk,
+                                                 int32_t num_splits) {
+  return dsa::sparse_mla_split_bytes(B * S, H, topk, num_splits);
 }
 
 extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices,
@@ -460,73 +581,30 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
                                   float sm_scale, int32_t is_causal, int32_t num_splits, void* out,
                                   float* lse, void* workspace, size_t workspace_bytes,
                                   void* stream) {
-  using namespace dsa;
-  if (d_v != kDV)
-    return set_error(kUnsupported, "dsa_sparse_mla_fwd: d_v must be 512 (got %d)", d_v);
-  if (d_qk != 576 && d_qk != 512)
-    return set_error(kUnsupported, "dsa_sparse_mla_fwd: d_qk must be 576 or 512 (got %d)", d_qk);
-  if (B < 0 || S < 0 || H <= 0 || topk < 0 || skv < 0)
-    return set_error(kInvalidArgument, "dsa_sparse_mla_fwd: bad sizes");
-  if (!(sm_scale > 0.f) || sm_scale == __builtin_inff())
-    return set_error(kInvalidArgument, "dsa_sparse_mla_fwd: sm_scale must be positive and finite");
-  if (block_table != nullptr && (block_size <= 0 || max_blocks <= 0))
-    return set_error(kInvalidArgument, "dsa_sparse_mla_fwd: paged KV needs block_size > 0 and max_blocks > 0");
-  const int64_t T = B * S;
-  if (T == 0) return kOk;
-  if (q == nullptr || kv == nullptr || indices == nullptr || out == nullptr)
-    return set_error(kInvalidArgument, "dsa_sparse_mla_fwd: null pointer");
-  if ((block_table ? skv : B * skv) >= ((int64_t)1 << 31))
-    return set_error(kUnsupported, "dsa_sparse_mla_fwd: more than 2^31 - 1 KV rows");
-
-  MlaParams p;
-  p.q = static_cast<const uint16_t*>(q);
-  p.kv = static_cast<const uint16_t*>(kv);
-  p.indices = indices;
-  p.block_table = block_table;
-  p.kv_len = kv_len;
-  p.q_start = q_start;
-  p.sink = attn_sink;
-  p.out = static_cast<uint16_t*>(out);
-  p.lse = lse;
-  p.skv = block_table ? (int64_t)max_blocks * block_size : skv;
-  p.pool_rows = skv;
-  p.B = (int)B;
-  p.S = (int)S;
-  p.H = H;
-  p.topk = topk;
-  p.block_size = block_size;
-  p.max_blocks = max_blocks;
-  p.scale_log2 = sm_scale * kLog2e;
-  p.causal = is_causal;
-
-  p.nhg = (H + kHeadsPerGroup - 1) / kHeadsPerGroup;
-  int ns = num_splits > 0 ? num_splits : choose_splits(T, p.nhg, topk);
-  if (topk == 0) ns = 1;
-  const int kps = topk > 0 ? (topk + ns - 1) / ns : 0;
-  if (kps > kMaxKeysPerSplit)
-    return set_error(kInvalidArgument, "dsa_sparse_mla_fwd: %d keys per split exceeds %d; raise num_splits",
-                     kps, kMaxKeysPerSplit);
-  p.nsplit = ns;
-  p.keys_per_split = kps;
-  if (ns > 1) {
-    const size_t need = (size_t)T * ns * H * (kDV + 1) * sizeof(float);
-    if (workspace == nullptr || workspace_bytes < need)
-      return set_error(kWorkspaceTooSmall, "dsa_sparse_mla_fwd: workspace of %zu bytes needed, %zu given",
-                       need, workspace_bytes);
-    p.part_o = static_cast<float*>(workspace);
-    p.part_lse = p.part_o + (size_t)T * ns * H * kDV;
-  } else {
-    p.part_o = nullptr;
-    p.part_lse = nullptr;
-  }
-  const int64_t units = T * ns;
-  const int64_t nblocks = ((units + kNumXcd - 1) / kNumXcd) * kNumXcd * p.nhg;
-  if (nblocks > 0x7fffffff) return set_error(kUnsupported, "dsa_sparse_mla_fwd: grid too large");
-  hipStream_t st = (hipStream_t)stream;
-  const int rc = d_qk == 576 ? launch_mla<576>(p, nblocks, st) : launch_mla<512>(p, nblocks, st);
-  if (rc != kOk || ns == 1) return rc;
-  const int64_t rows = T * H;
-  hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, st,
-                     p.part_o, p.part_lse, rows, H, ns, p.out, lse);
-  return check_launch("dsa_sparse_mla_fwd(combine)");
+  dsa::MlaRun r{};
+  r.q = q;
+  r.kv = kv;
+  r.indices = indices;
+  r.block_table = block_table;
+  r.kv_len = kv_len;
+  r.q_start = q_start;
+  r.attn_sink = attn_sink;
+  r.B = B;
+  r.S = S;
+  r.H = H;
+  r.d_qk = d_qk;
+  r.d_v = d_v;
+  r.skv = skv;
+  r.block_size = block_size;
+  r.max_blocks = max_blocks;
+  r.topk = topk;
+  r.sm_scale = sm_scale;
+  r.is_causal = is_causal;
+  r.num_splits = num_splits;
+  r.out = out;
+  r.lse = lse;
+  r.workspace = workspace;
+  r.workspace_bytes = workspace_bytes;
+  r.stream = stream;
+  return dsa::sparse_mla_run(r, "dsa_sparse_mla_fwd");
 }

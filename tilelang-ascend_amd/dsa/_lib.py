@@ -40,6 +40,10 @@ SIGNATURES = {
     "dsa_sparse_mla_fwd": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32,
                                    c_i32, c_i32, c_i64, c_i32, c_i32, c_i32, c_f32, c_i32, c_i32,
                                    c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "dsa_sparse_flash_mla_workspace_bytes": (c_sz, [c_i64, c_i32, c_i32, c_i32]),
+    "dsa_sparse_flash_mla": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i32, c_vp,
+                                     c_i32, c_vp, c_i64, c_i32, c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_f32,
+                                     c_i32, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "dsa_act_quant_int8": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp]),
     "dsa_quant_fp8_rows": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "dsa_indexer_k_append_fp8": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp]),

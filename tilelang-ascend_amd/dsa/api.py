@@ -564,3 +564,93 @@ def indexer_q_quant_fp8(query: torch.Tensor, weights: torch.Tensor) -> Tuple[tor
     check(lib().dsa_indexer_q_quant_fp8(_ptr(query), _ptr(w), T, N1, D, _ptr(q8), _ptr(wo), _stream(dev)),
           "dsa_indexer_q_quant_fp8")
     return q8, wo
+
+
+# ---------------------------------------------------------------------------
+# DeepSeek-V4 sparse flash MLA (sliding window + compressed KV, sinks)
+# ---------------------------------------------------------------------------
+def sparse_flash_mla(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Tensor] = None,
+                     cmp_sparse_indices: Optional[torch.Tensor] = None, ori_block_table: torch.Tensor,
+                     cmp_block_table: Optional[torch.Tensor] = None, cu_seqlens_q: Optional[torch.Tensor] = None,
+                     seqused_q: Optional[torch.Tensor] = None, seqused_kv: torch.Tensor, sinks: torch.Tensor,
+                     softmax_scale: float, cmp_ratio: Optional[int] = None, ori_mask_mode: int = 4,
+                     cmp_mask_mode: int = 3, ori_win_left: int = 127, ori_win_right: int = 0,
+                     layout_q: str = "TND", layout_kv: str = "PA_ND", return_softmax_lse: bool = False,
+                     core_num: Optional[int] = None, topk_cmp: Optional[int] = None):
+    """DeepSeek-V4 sparse flash MLA with the signature, checks and outputs of
+    ``sparse_flash_mla`` (examples/deepseek_v4/sparse_flash_mla/sparse_flash_mla_api.py:94-253):
+    scenario 1 (``cmp_kv`` None) attends to a window of ``ori_win_left + 1`` original
+    keys, scenario 2 (``cmp_kv`` without ``cmp_sparse_indices``) also to every visible
+    compressed key, scenario 3 to the listed compressed keys; sinks in the softmax
+    denominator, K = V.  Semantics of sparse_flash_mla_golden.py:56-153.  ``core_num``
+    and ``seqused_q`` are accepted and unused, as in the reference."""
+    del seqused_q, core_num
+    assert ori_mask_mode == 4, "only ori_mask_mode=4 supported"
+    assert cmp_mask_mode == 3 or cmp_kv is None, "only cmp_mask_mode=3 supported"
+    assert ori_win_right == 0, "only ori_win_right=0 supported"
+    assert layout_kv == "PA_ND", "only layout_kv=PA_ND supported"
+    assert layout_q in ("TND", "BSND"), f"unsupported layout_q={layout_q!r}"
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"q must be bfloat16 (the built kernel), got {q.dtype}")
+    scenario = 1 if cmp_kv is None else (2 if cmp_sparse_indices is None else 3)
+    # the small tensors (tables, lengths, sinks, lists) may live anywhere: they are
+    # moved to q's device, as sparse_flash_mla_api.py:186-214 does
+    dev = _require_gpu(q, ori_kv, cmp_kv)
+    if layout_q == "TND":
+        assert cu_seqlens_q is not None, "cu_seqlens_q is required for TND"
+        cu = cu_seqlens_q.to(torch.int64).cpu()
+        B = cu.numel() - 1
+        T, N1, D = q.shape
+        seq_lens = (cu[1:] - cu[:-1]).tolist()
+        q_prefix = cu[:-1].to(torch.int32)
+        S_max = None
+    else:
+        B, S_max, N1, D = q.shape
+        T = B * S_max
+        q_prefix = torch.arange(B, dtype=torch.int32) * S_max
+        seq_lens = [S_max] * B
+        if cu_seqlens_q is not None:
+            cu = cu_seqlens_q.to(torch.int64).cpu()
+            seq_lens = (cu[1:] - cu[:-1]).tolist()
+    N2 = ori_kv.shape[2]
+    if scenario == 3:
+        ci = cmp_sparse_indices.to(torch.int32)
+        N2 = ci.shape[-2]
+        K = topk_cmp if topk_cmp is not None else ci.shape[-1]
+        assert ci.shape[-1] == K, "topk_cmp does not match cmp_sparse_indices last dim"
+        cmp_idx = ci.reshape(T, N2, K)[:, 0, :].contiguous().to(dev)
+        n_cmp = K
+    elif scenario == 2:
+        N2 = cmp_kv.shape[2]
+        cmp_idx, K = None, 0
+        n_cmp = int(seqused_kv.max().item()) // cmp_ratio
+    else:
+        cmp_idx, K, n_cmp = None, 0, 0
+    if N1 != 64 or N2 != 1 or D != 512:
+        raise ValueError(f"only N1=64, N2=1, D=512 supported (got N1={N1}, N2={N2}, D={D})")
+    for name, t in (("q", q), ("ori_kv", ori_kv)) + ((("cmp_kv", cmp_kv),) if cmp_kv is not None else ()):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+        _require_contiguous(name, t)
+    ori_bt = ori_block_table.to(device=dev, dtype=torch.int32).contiguous()
+    cmp_bt = cmp_block_table.to(device=dev, dtype=torch.int32).contiguous() if cmp_kv is not None else None
+    act_q = torch.tensor(seq_lens, dtype=torch.int32, device=dev)
+    qp = q_prefix.to(dev)
+    kvl = seqused_kv.to(device=dev, dtype=torch.int32).contiguous()
+    sk = sinks.to(device=dev, dtype=torch.float32).contiguous()
+    out = torch.empty((T, N1, D), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((T, N1), dtype=torch.float32, device=dev)
+    L = lib()
+    wsb = L.dsa_sparse_flash_mla_workspace_bytes(T, N1, ori_win_left, n_cmp)
+    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+    cb, cbs, ctl = (cmp_kv.shape[0], cmp_kv.shape[1], cmp_bt.shape[1]) if cmp_kv is not None else (0, 0, 0)
+    check(L.dsa_sparse_flash_mla(_ptr(q), T, N1, D, _ptr(qp), _ptr(act_q), _ptr(kvl), B, _ptr(ori_kv),
+                                 ori_kv.shape[0], ori_kv.shape[1], _ptr(ori_bt), ori_bt.shape[1], _ptr(cmp_kv), cb,
+                                 cbs, _ptr(cmp_bt), ctl, _ptr(cmp_idx), K, n_cmp,
+                                 int(cmp_ratio) if cmp_ratio is not None else 0, _ptr(sk), float(softmax_scale),
+                                 ori_win_left, _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev)),
+          "dsa_sparse_flash_mla")
+    if layout_q == "BSND":
+        out = out.view(B, S_max, N1, D)
+        lse = lse.view(B, S_max, N1)
+    return (out, lse) if return_softmax_lse else out

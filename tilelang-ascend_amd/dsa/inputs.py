@@ -95,3 +95,61 @@ def indexer_fp8(B=1, S1=4096, S2=32768, H=64, D=128, seed=2, device="cpu"):
     scale = torch.clamp(scale, min=torch.finfo(torch.float32).tiny)
     k = (k32 / scale.unsqueeze(-1)).to(FP8)
     return dict(q=q.contiguous(), k=k.contiguous(), w=w.contiguous(), key_scale=scale.view(B, S2).contiguous())
+
+
+def flash_mla_v4(scenario=3, B=1, S1=1024, N1=64, D=512, K=512, cmp_ratio=4, block_size=128,
+                 seqused_kv=None, cu_seqlens_q=None, seed=42, win_left=127):
+    """A DeepSeek-V4 sparse flash MLA case shaped like the reference's fast scenarios
+    (sparse_flash_mla_golden.py:384-461: "swa" scenario 1, "hca" 2 with cmp_ratio
+    128, "csa" 3 with K = 512): TND queries (cu_seqlens_q), q ~ U(-10, 10), original
+    keys ~ U(-10, 10) and compressed keys ~ U(-5, 10) in shuffled pages of
+    ``block_size``, sinks ~ U(-1, 1), per-row top-K compressed lists (a random
+    permutation of the visible compressed positions, -1 padded).  Draw order:
+    q, original keys, page permutation, compressed keys, its permutation, lists, sinks."""
+    g = _gen(seed, "cpu")
+    if cu_seqlens_q is None:
+        cu_seqlens_q = [S1 * i for i in range(B + 1)]
+    lens = [cu_seqlens_q[i + 1] - cu_seqlens_q[i] for i in range(B)]
+    if seqused_kv is None:
+        seqused_kv = list(lens)
+    T = cu_seqlens_q[-1]
+    bf = torch.bfloat16
+    q = (torch.rand((T, N1, D), generator=g) * 20 - 10).to(bf)
+
+    def paged(n_tok, lo, hi):
+        mx = max(max(n_tok), 1)
+        logical = (torch.rand((B, mx, D), generator=g) * (hi - lo) + lo).to(bf)
+        nbs = [(n + block_size - 1) // block_size for n in n_tok]
+        nblocks = max(sum(nbs), 1) + 2
+        perm = torch.randperm(nblocks, generator=g)
+        table = torch.full((B, max(max(nbs), 1)), -1, dtype=torch.int32)
+        pool = torch.zeros((nblocks, block_size, 1, D), dtype=bf)
+        c = 0
+        for b in range(B):
+            for i in range(nbs[b]):
+                page = int(perm[c]); c += 1
+                table[b, i] = page
+                lo_, hi_ = i * block_size, min((i + 1) * block_size, n_tok[b])
+                pool[page, :hi_ - lo_, 0] = logical[b, lo_:hi_]
+        return pool, table
+
+    ori_pa, ori_bt = paged(seqused_kv, -10, 10)
+    case = dict(q=q, ori_kv=ori_pa, ori_block_table=ori_bt, cu_seqlens_q=torch.tensor(cu_seqlens_q, dtype=torch.int32),
+                seqused_kv=torch.tensor(seqused_kv, dtype=torch.int32), cmp_kv=None, cmp_block_table=None,
+                cmp_sparse_indices=None, cmp_ratio=cmp_ratio if scenario >= 2 else None,
+                softmax_scale=0.04419417, ori_win_left=win_left, topk_cmp=None)
+    if scenario >= 2:
+        cmp_seqs = [n // cmp_ratio for n in seqused_kv]
+        case["cmp_kv"], case["cmp_block_table"] = paged(cmp_seqs, -5, 10)
+    if scenario == 3:
+        idx = torch.full((T, 1, K), -1, dtype=torch.int32)
+        for b in range(B):
+            for s in range(lens[b]):
+                cur = max(0, (seqused_kv[b] - lens[b] + s + 1) // cmp_ratio)
+                perm = torch.randperm(cur, generator=g).to(torch.int32) if cur > 0 else torch.empty(0, dtype=torch.int32)
+                take = min(cur, K)
+                idx[cu_seqlens_q[b] + s, 0, :take] = perm[:take]
+        case["cmp_sparse_indices"] = idx
+        case["topk_cmp"] = K
+    case["sinks"] = torch.rand(N1, generator=g) * 2 - 1
+    return case
