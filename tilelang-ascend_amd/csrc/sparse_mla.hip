@@ -60,8 +60,9 @@ struct MlaParams {
   const float* sink;            // [H] or null
   uint16_t* out;                // [T, H, 512]
   float* lse;                   // [T, H] or null
-  float* part_o;                // [T, nsplit, H, 512]
+  uint16_t* part_o;             // fp16 [T, nsplit, H, 512]: the normalised partial output / part_scale
   float* part_lse;              // [T, nsplit, H]
+  float* part_scale;            // [T, nsplit, H]: a power of two >= the row's largest |output|
   int64_t skv;                  // keys per batch row (non-paged) or max_blocks * bs
   int64_t pool_rows;            // rows in the page pool (paged)
   const uint16_t* kv2;          // second row pool (direct rows with the kRowTag2 bit) or null
@@ -108,14 +109,20 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   int32_t* rows = reinterpret_cast<int32_t*>(smem + kStages * STAGE);  // [keys_per_split]
 
-  // ---- workgroup -> (token, head group, split); head groups of one (token,
-  // split) share an XCD so the second gather of the same rows hits L2.
+  // ---- workgroup -> (token, head group, split).  Workgroup ids are dealt to
+  // the 8 XCDs round-robin; XCD x takes a contiguous range of (token, split)
+  // units, so the head groups and splits of one token share that XCD's L2 (q is
+  // fetched once per token, a second gather of the same rows hits, the partial
+  // results stay close to the combine) and neighbouring tokens, whose index
+  // sets overlap, do too.
   const int bid = blockIdx.x;
   const int xcd = bid % dsa::kNumXcd, r = bid / dsa::kNumXcd;
   const int hg = r % p.nhg;
-  const int64_t x = (int64_t)(r / p.nhg) * dsa::kNumXcd + xcd;
   const int64_t T = (int64_t)p.B * p.S;
-  if (x >= T * p.nsplit) return;
+  const int64_t units = T * p.nsplit;
+  const int64_t per_xcd = (units + dsa::kNumXcd - 1) / dsa::kNumXcd;
+  const int64_t x = (int64_t)xcd * per_xcd + r / p.nhg;
+  if (x >= units || r / p.nhg >= per_xcd) return;
   const int64_t token = x / p.nsplit;
   const int split = (int)(x % p.nsplit);
   const int b = (int)(token / p.S), s = (int)(token % p.S);
@@ -396,21 +403,40 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
     }
     if (g == 0 && p.lse) p.lse[token * p.H + head] = lse_v;
   } else {
+    // fp16 partials scaled by a power of two per (token, head): 2 bytes per value
+    // instead of 4 and a relative error of 2^-12 of the row's largest entry
     const int64_t prow = (token * p.nsplit + split) * p.H + head;
-    float* op = p.part_o + prow * kDV + 4 * g;
+    float amax = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < kDV / 16; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fabsf(o[dt][i]));
+    amax = xor32_max(xor16_max(amax)) * inv;
+    int e = 0;
+    if (amax > 0.f) (void)frexpf(amax, &e);  // amax = m 2^e, m in [0.5, 1)
+    const float down = ldexpf(inv, -e);       // o * inv / 2^e
+    uint16_t* op = p.part_o + prow * kDV + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < kDV / 16; ++dt) {
-      dsa::f32x4 v = {o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv};
-      *reinterpret_cast<dsa::f32x4*>(op + 16 * dt) = v;
+      const _Float16 h0 = (_Float16)(o[dt][0] * down), h1 = (_Float16)(o[dt][1] * down);
+      const _Float16 h2 = (_Float16)(o[dt][2] * down), h3 = (_Float16)(o[dt][3] * down);
+      dsa::i32x2 v;
+      v[0] = (int)((uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16));
+      v[1] = (int)((uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16));
+      *reinterpret_cast<dsa::i32x2*>(op + 16 * dt) = v;
     }
-    if (g == 0) p.part_lse[prow] = lse_v;
+    if (g == 0) {
+      p.part_lse[prow] = lse_v;
+      p.part_scale[prow] = ldexpf(1.f, e);
+    }
   }
 }
 
 // Merge split partials: lse = logsumexp_p lse_p, out = sum_p exp(lse_p - lse) out_p.
 // One 128-thread group per (token, head); each thread owns 4 consecutive dims.
-__global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restrict__ part_o,
+__global__ __launch_bounds__(256) void mla_combine_kernel(const uint16_t* __restrict__ part_o,
                                                           const float* __restrict__ part_lse,
+                                                          const float* __restrict__ part_scale,
                                                           int64_t rows, int H, int nsplit,
                                                           uint16_t* __restrict__ out,
                                                           float* __restrict__ lse) {
@@ -419,18 +445,42 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
   const int d4 = threadIdx.x & 127;
   const int64_t token = rh / H;
   const int head = (int)(rh % H);
+  // up to kU splits per batch: their loads are all issued before any is used
+  constexpr int kU = 8;
   float mx = -__builtin_inff();
-  for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, part_lse[(token * nsplit + sp) * H + head]);
+  for (int sp0 = 0; sp0 < nsplit; sp0 += kU) {
+    float l[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      l[u] = sp0 + u < nsplit ? part_lse[(token * nsplit + sp0 + u) * H + head] : -__builtin_inff();
+#pragma unroll
+    for (int u = 0; u < kU; ++u) mx = fmaxf(mx, l[u]);
+  }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   float den = 0.f;
   if (mx != -__builtin_inff()) {
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const int64_t prow = (token * nsplit + sp) * H + head;
-      const float wgt = __expf(part_lse[prow] - mx);
-      den += wgt;
-      const dsa::f32x4 v = *reinterpret_cast<const dsa::f32x4*>(part_o + prow * kDV + 4 * d4);
+    for (int sp0 = 0; sp0 < nsplit; sp0 += kU) {
+      float l[kU], sc[kU];
+      dsa::i32x2 v[kU];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] += wgt * v[i];
+      for (int u = 0; u < kU; ++u) {
+        const bool ok = sp0 + u < nsplit;
+        const int64_t prow = (token * nsplit + sp0 + u) * H + head;
+        l[u] = ok ? part_lse[prow] : -__builtin_inff();
+        sc[u] = ok ? part_scale[prow] : 0.f;
+        v[u] = ok ? *reinterpret_cast<const dsa::i32x2*>(part_o + prow * kDV + 4 * d4) : dsa::i32x2{0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const float wgt = l[u] == -__builtin_inff() ? 0.f : __expf(l[u] - mx);
+        den += wgt;
+        const float ws = wgt * sc[u];
+        const uint32_t w0 = (uint32_t)v[u][0], w1 = (uint32_t)v[u][1];
+        acc[0] += ws * (float)__builtin_bit_cast(_Float16, (uint16_t)(w0 & 0xffffu));
+        acc[1] += ws * (float)__builtin_bit_cast(_Float16, (uint16_t)(w0 >> 16));
+        acc[2] += ws * (float)__builtin_bit_cast(_Float16, (uint16_t)(w1 & 0xffffu));
+        acc[3] += ws * (float)__builtin_bit_cast(_Float16, (uint16_t)(w1 >> 16));
+      }
     }
   }
   const float inv = den > 0.f ? 1.f / den : 0.f;
@@ -484,7 +534,7 @@ size_t sparse_mla_split_bytes(int64_t T, int32_t H, int32_t topk, int32_t num_sp
   const int nhg = (H + kHeadsPerGroup - 1) / kHeadsPerGroup;
   const int ns = num_splits > 0 ? num_splits : choose_splits(T, nhg, topk);
   if (ns <= 1) return 0;
-  return (size_t)T * ns * H * (kDV + 1) * sizeof(float);
+  return (size_t)T * ns * H * (kDV * sizeof(uint16_t) + 2 * sizeof(float));
 }
 
 int sparse_mla_run(const MlaRun& r, const char* what) {
@@ -544,15 +594,17 @@ int sparse_mla_run(const MlaRun& r, const char* what) {
   p.nsplit = ns;
   p.keys_per_split = kps;
   if (ns > 1) {
-    const size_t need = (size_t)T * ns * r.H * (kDV + 1) * sizeof(float);
+    const size_t need = (size_t)T * ns * r.H * (kDV * sizeof(uint16_t) + 2 * sizeof(float));
     if (r.workspace == nullptr || r.workspace_bytes < need)
       return set_error(kWorkspaceTooSmall, "%s: workspace of %zu bytes needed, %zu given", what, need,
                        r.workspace_bytes);
-    p.part_o = static_cast<float*>(r.workspace);
-    p.part_lse = p.part_o + (size_t)T * ns * r.H * kDV;
+    p.part_o = static_cast<uint16_t*>(r.workspace);
+    p.part_lse = reinterpret_cast<float*>(p.part_o + (size_t)T * ns * r.H * kDV);
+    p.part_scale = p.part_lse + (size_t)T * ns * r.H;
   } else {
     p.part_o = nullptr;
     p.part_lse = nullptr;
+    p.part_scale = nullptr;
   }
   const int64_t units = T * ns;
   const int64_t nblocks = ((units + kNumXcd - 1) / kNumXcd) * kNumXcd * p.nhg;
@@ -562,7 +614,7 @@ int sparse_mla_run(const MlaRun& r, const char* what) {
   if (rc != kOk || ns == 1) return rc;
   const int64_t rows = T * r.H;
   hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, st,
-                     p.part_o, p.part_lse, rows, r.H, ns, p.out, r.lse);
+                     p.part_o, p.part_lse, p.part_scale, rows, r.H, ns, p.out, r.lse);
   return check_launch("dsa_sparse_mla_fwd(combine)");
 }
 
