@@ -261,11 +261,47 @@ def target_configs(L, steps: int) -> dict:
     del kb, k8, ks, qb, wq, q8, wo
     torch.cuda.empty_cache()
     res["flash_mla_v4"] = flash_mla_v4_configs(L, steps)
+    res["block_sparse_indexer"] = block_sparse_indexer_configs(L, steps)
     res["fp8_producers"] = {"key_cache_128k_us": round(uk, 2),
                             "key_cache_frac_of_hbm": round(kbytes / uk / 1e3 / PEAK_HBM_GBS, 4),
                             "query_4096_us": round(uq, 2),
                             "query_frac_of_hbm": round(qbytes / uq / 1e3 / PEAK_HBM_GBS, 4),
                             "algorithmic_bytes": {"key_cache": kbytes, "query": qbytes}}
+    return res
+
+
+def block_sparse_indexer_configs(L, steps: int) -> dict:
+    """Block-sparse indexer logits (examples/HISA/paged_block_sparse_mqa_attn_expert.py):
+    the reference test's defaults (batch 1, one token, 32 heads x 128, 128-key blocks,
+    top-64 blocks of a 1024-block cache) and a decode batch of 64 tokens with the
+    same shapes; HBM bound: 256 B per key read + 4 B per logit written."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream(dev).cuda_stream
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(8)
+    for name, batch in (("reference_default", 1), ("decode_b64", 64)):
+        H, bs, topk, nb = 32, 128, 64, 1024
+        q = torch.rand((batch, H, 128), generator=g, device=dev).half()
+        kv = torch.rand((nb, bs, 1, 128), generator=g, device=dev).half()
+        w = torch.rand((batch, H), generator=g, device=dev).half()
+        ctx = torch.full((batch,), nb * bs, dtype=torch.int32, device=dev)
+        bt = torch.stack([torch.randperm(nb, generator=g, device=dev) for _ in range(batch)]).int()
+        idx = torch.randint(0, nb, (batch, topk), generator=g, device=dev, dtype=torch.int32)
+        out = torch.empty((batch, topk, bs), dtype=torch.float32, device=dev)
+
+        def run():
+            rc = L.dsa_block_sparse_indexer_logits(q.data_ptr(), kv.data_ptr(), idx.data_ptr(), w.data_ptr(),
+                                                   ctx.data_ptr(), bt.data_ptr(), batch, 1, H, 128, topk, nb, bs, nb,
+                                                   0, out.data_ptr(), st)
+            if rc != 0:
+                raise RuntimeError(L.dsa_last_error().decode())
+
+        us = _time_launches(run, steps)
+        byts = batch * topk * bs * (256 + 4) + batch * H * 258
+        res[name] = {"us": round(us, 2), "gbs": round(byts / us / 1e3, 1),
+                     "frac_of_hbm": round(byts / us / 1e3 / PEAK_HBM_GBS, 4)}
     return res
 
 

@@ -198,6 +198,26 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices,
                        void* stream);
 
 /*
+ * Block-sparse indexer logits (the HISA second stage): replaces the call of
+ * paged_block_sparse_mqa_attn_return_logits
+ * (examples/HISA/paged_block_sparse_mqa_attn_expert.py:54-422; reference
+ * ref_paged_block_sparse_mqa_attn :425-468).
+ *   q [batch * seq_len, heads, 128], weights [batch * seq_len, heads] (fp16, or
+ *   bf16 with is_bf16 = 1); kv_cache [num_phys_blocks, kv_block_size, 1, 128];
+ *   topk_block_indices [batch * seq_len, topk] logical blocks, block_tables
+ *   [batch, max_blocks], context_lens [batch] int32.
+ *   logits [batch * seq_len, topk, kv_block_size] fp32:
+ *   sum_h w_h ReLU(q_h . k_j), -inf at positions >= context_lens[b] (and for a
+ *   block id outside the table or a missing page).  heads in {16, 32, 48, 64},
+ *   kv_block_size a multiple of 16.
+ */
+int dsa_block_sparse_indexer_logits(const void* q, const void* kv_cache, const int32_t* topk_block_indices,
+                                    const void* weights, const int32_t* context_lens, const int32_t* block_tables,
+                                    int64_t batch, int64_t seq_len, int32_t heads, int32_t index_dim, int32_t topk,
+                                    int64_t num_phys_blocks, int32_t kv_block_size, int32_t max_blocks,
+                                    int32_t is_bf16, float* logits, void* stream);
+
+/*
  * DeepSeek-V4 sparse flash MLA: sliding window over the original KV plus the
  * compressed KV, with sinks.  Replaces the call behind sparse_flash_mla
  * (examples/deepseek_v4/sparse_flash_mla/sparse_flash_mla_api.py:94-253; kernel

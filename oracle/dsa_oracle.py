@@ -391,6 +391,35 @@ def lse_combine(outs: Sequence[torch.Tensor], lses: Sequence[torch.Tensor]):
 
 
 # ---------------------------------------------------------------------------
+# block-sparse indexer logits (HISA second stage)
+# ---------------------------------------------------------------------------
+def block_sparse_indexer_logits(q: torch.Tensor, kv_cache: torch.Tensor, topk_block_indices: torch.Tensor,
+                                weights: torch.Tensor, context_lens: torch.Tensor,
+                                block_tables: torch.Tensor) -> torch.Tensor:
+    """``ref_paged_block_sparse_mqa_attn`` (examples/HISA/paged_block_sparse_mqa_attn_expert.py:425-468)
+    restated over tokens: q ``[B, S, H, D]``, kv_cache ``[blocks, bs, 1, D]``,
+    indices ``[B, S, topk]`` logical blocks -> fp32 ``[B, S, topk * bs]``; score
+    ``sum_h w_h ReLU(q_h . k)`` of each key of the block, -inf at positions
+    ``>= context_lens[b]``."""
+    B, S, H, D = q.shape
+    topk = topk_block_indices.shape[-1]
+    bs = kv_cache.shape[1]
+    out = torch.empty((B, S, topk, bs), dtype=torch.float32)
+    pos = torch.arange(bs)
+    for b in range(B):
+        ctx = int(context_lens[b])
+        for s in range(S):
+            lb = topk_block_indices[b, s].long()                       # [topk]
+            pages = block_tables[b, lb].long()
+            keys = kv_cache[pages, :, 0, :].float()                    # [topk, bs, D]
+            sc = torch.relu(torch.einsum("hd,tjd->thj", q[b, s].float(), keys))
+            logit = (sc * weights[b, s].float().view(1, H, 1)).sum(dim=1)   # [topk, bs]
+            logit[(lb.view(-1, 1) * bs + pos.view(1, -1)) >= ctx] = NEG_INF
+            out[b, s] = logit
+    return out.view(B, S, topk * bs)
+
+
+# ---------------------------------------------------------------------------
 # DeepSeek-V4 sparse flash MLA (window over the original KV + compressed KV)
 # ---------------------------------------------------------------------------
 def v4_compressed_positions(cmp_sparse_indices: Optional[torch.Tensor], b: int, s: int, act_kv: int, act_q: int,
@@ -561,6 +590,8 @@ PINNED_BY = {
                    "invariance; LSE == logsumexp (tests/test_oracle_mla.py)",
     "sparse_mla_fwd_dense": "agreement with the gather form and brute force",
     "lse_combine": "split a row's index set in two, combine == unsplit result",
+    "block_sparse_indexer_logits": "the a1 restatement (indexer_scores) on the gathered blocks' keys "
+                   "(independent code), masked positions (tests/test_oracle_indexer.py)",
     "sparse_flash_mla_v4": "the gather formulation on the same key sets (independent code), "
                    "closed forms (no key: out 0 and lse = sink; one key: out = v e^s / (e^s + e^sink)), "
                    "compressed-position rules against hand-worked lists (tests/test_oracle_mla.py)",

@@ -210,3 +210,27 @@ def test_paged_keys_equal_contiguous(block_size):
                                     layout_key="PA_BSND", sparse_count=K)
     assert torch.equal(ipa, ic)
     assert torch.equal(torch.nan_to_num(spa, neginf=-1.0), torch.nan_to_num(sc, neginf=-1.0))
+
+
+def test_block_sparse_logits_equal_indexer_scores_on_gathered_blocks():
+    # HISA logits (examples/HISA/paged_block_sparse_mqa_attn_expert.py:425-468) against
+    # the lightning-indexer score restatement run on the same keys gathered contiguously
+    from oracle.dsa_oracle import block_sparse_indexer_logits
+    g = torch.Generator().manual_seed(12)
+    B, S, H, D, bs, topk, nb = 2, 3, 8, 16, 4, 5, 12
+    q = torch.randn((B, S, H, D), generator=g)
+    kv = torch.randn((nb, bs, 1, D), generator=g)
+    w = torch.rand((B, S, H), generator=g)
+    bt = torch.stack([torch.randperm(nb, generator=g)[:6] for _ in range(B)]).int()
+    ctx = torch.tensor([21, 9], dtype=torch.int32)
+    idx = torch.randint(0, 6, (B, S, topk), generator=g, dtype=torch.int32)
+    got = block_sparse_indexer_logits(q, kv, idx, w, ctx, bt).view(B, S, topk, bs)
+    for b in range(B):
+        for s in range(S):
+            for i in range(topk):
+                lb = int(idx[b, s, i])
+                keys = kv[int(bt[b, lb]), :, 0, :]
+                ref = indexer_scores(q[b, s].unsqueeze(0), keys, w[b, s].unsqueeze(0), 1, bs, 0)[0]
+                pos = lb * bs + torch.arange(bs)
+                ref = torch.where(pos < int(ctx[b]), ref, torch.tensor(float("-inf")))
+                torch.testing.assert_close(got[b, s, i], ref, rtol=1e-5, atol=1e-5)

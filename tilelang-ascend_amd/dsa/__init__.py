@@ -6,10 +6,12 @@ HIP kernels for gfx950 behind the C ABI in include/dsa_mi355x.h."""
 from .api import (  # noqa: F401
     act_quant,
     act_quant_kernel_int8_optimized,
+    block_sparse_indexer_logits,
     indexer_k_append_fp8,
     indexer_logits,
     indexer_q_quant_fp8,
     lightning_indexer,
+    paged_block_sparse_mqa_attn_return_logits,
     paged_slots,
     quant_fp8,
     simple_topk_selector,
@@ -23,6 +25,6 @@ from ._lib import DSAError, LIB_PATH, lib  # noqa: F401
 __all__ = [
     "lightning_indexer", "indexer_logits", "topk_selector", "simple_topk_selector",
     "sparse_mla_fwd", "sparse_attention_fwd", "act_quant", "act_quant_kernel_int8_optimized",
-    "sparse_flash_mla", "quant_fp8", "paged_slots", "indexer_k_append_fp8", "indexer_q_quant_fp8",
+    "sparse_flash_mla", "block_sparse_indexer_logits", "paged_block_sparse_mqa_attn_return_logits", "quant_fp8", "paged_slots", "indexer_k_append_fp8", "indexer_q_quant_fp8",
     "DSAError", "LIB_PATH", "lib",
 ]

@@ -44,6 +44,8 @@ SIGNATURES = {
     "dsa_sparse_flash_mla": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i32, c_vp,
                                      c_i32, c_vp, c_i64, c_i32, c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_f32,
                                      c_i32, c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "dsa_block_sparse_indexer_logits": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32, c_i32, c_i32,
+                                                c_i64, c_i32, c_i32, c_i32, c_vp, c_vp]),
     "dsa_act_quant_int8": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp]),
     "dsa_quant_fp8_rows": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "dsa_indexer_k_append_fp8": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp]),

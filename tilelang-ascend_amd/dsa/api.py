@@ -654,3 +654,62 @@ def sparse_flash_mla(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[
         out = out.view(B, S_max, N1, D)
         lse = lse.view(B, S_max, N1)
     return (out, lse) if return_softmax_lse else out
+
+
+# ---------------------------------------------------------------------------
+# block-sparse indexer logits (HISA second stage)
+# ---------------------------------------------------------------------------
+def block_sparse_indexer_logits(q: torch.Tensor, kv_cache: torch.Tensor, topk_block_indices: torch.Tensor,
+                                weights: torch.Tensor, context_lens: torch.Tensor,
+                                block_tables: torch.Tensor) -> torch.Tensor:
+    """Indexer logits of every key in each token's top-k logical key blocks:
+    q ``[T, heads, 128]`` (fp16 or bf16), kv_cache ``[blocks, block_size, 1, 128]``,
+    topk_block_indices ``[T, topk]``, weights ``[T, heads]``, context_lens ``[batch]``,
+    block_tables ``[batch, max_blocks]`` (T = batch * seq_len, token t in batch
+    t // seq_len) -> fp32 ``[T, topk, block_size]``, ``sum_h w_h ReLU(q_h . k)`` and
+    -inf at positions past the context (examples/HISA/paged_block_sparse_mqa_attn_expert.py:425-468)."""
+    if q.dim() != 3 or kv_cache.dim() != 4 or kv_cache.shape[2] != 1:
+        raise ValueError("q must be [T, heads, dim] and kv_cache [blocks, block_size, 1, dim]")
+    if q.dtype not in (torch.float16, torch.bfloat16) or kv_cache.dtype != q.dtype:
+        raise ValueError(f"q and kv_cache must both be float16 or bfloat16, got {q.dtype} and {kv_cache.dtype}")
+    T, H, D = q.shape
+    B = context_lens.numel()
+    if B == 0 or T % B != 0:
+        raise ValueError(f"{T} tokens do not split evenly over {B} batches")
+    topk = topk_block_indices.shape[-1]
+    dev = _require_gpu(q, kv_cache)
+    for name, t in (("q", q), ("kv_cache", kv_cache)):
+        _require_contiguous(name, t)
+    w = weights.to(device=dev, dtype=q.dtype).contiguous()
+    if tuple(w.shape) != (T, H):
+        raise ValueError(f"weights must be [T, heads] = {(T, H)}, got {tuple(w.shape)}")
+    blk = topk_block_indices.to(device=dev, dtype=torch.int32).contiguous().view(T, topk)
+    ctx = context_lens.to(device=dev, dtype=torch.int32).contiguous()
+    bt = block_tables.to(device=dev, dtype=torch.int32).contiguous()
+    bs = kv_cache.shape[1]
+    out = torch.empty((T, topk, bs), dtype=torch.float32, device=dev)
+    check(lib().dsa_block_sparse_indexer_logits(_ptr(q), _ptr(kv_cache), _ptr(blk), _ptr(w), _ptr(ctx), _ptr(bt), B,
+                                                T // B, H, D, topk, kv_cache.shape[0], bs, bt.shape[1],
+                                                int(q.dtype == torch.bfloat16), _ptr(out), _stream(dev)),
+          "dsa_block_sparse_indexer_logits")
+    return out
+
+
+def paged_block_sparse_mqa_attn_return_logits(batch: int, seq_len: int, num_phys_blocks: int, kv_block_size: int,
+                                              topk: int, heads: int, index_dim: int, max_blocks: int,
+                                              num_stages: int = 2, threads: int = 2) -> Callable:
+    """Factory with the signature of the reference's JIT kernel
+    (examples/HISA/paged_block_sparse_mqa_attn_expert.py:54-66): returns
+    ``kernel(q [T, heads, dim], kv_cache, topk_block_indices [T, topk], weights [T, heads],
+    context_lens, block_tables) -> logits [T, topk, kv_block_size]`` (its ``out_idx=[3]``)."""
+    del num_stages, threads
+    assert topk % 4 == 0, "topk must be divisible by 4"
+
+    def kernel(q, kv_cache, topk_block_indices, weights, context_lens, block_tables):
+        if q.shape != (batch * seq_len, heads, index_dim) or kv_cache.shape[:2] != (num_phys_blocks, kv_block_size):
+            raise ValueError("inputs do not match the kernel's batch, seq_len, heads, index_dim or cache shape")
+        if topk_block_indices.shape[-1] != topk or block_tables.shape[-1] != max_blocks:
+            raise ValueError("topk_block_indices / block_tables do not match topk / max_blocks")
+        return block_sparse_indexer_logits(q, kv_cache, topk_block_indices, weights, context_lens, block_tables)
+
+    return kernel
