@@ -261,3 +261,52 @@ def test_long_rows_group_max_selection(gpu, S2, mode):
         qk = torch.relu(torch.einsum("hd,sd->hs", inp["q"][0, t].float(), kdq[0, :n, 0]))
         ref = (inp["w"][0, t].unsqueeze(1) * qk).sum(0)
         _logit_close(lg[t, :n], ref)
+
+
+def test_group_maxima_are_exact(gpu):
+    # the indexer's 16-key group maxima equal the maxima of the logits it wrote
+    # (every group that holds a visible key; -inf past a row's causal length)
+    from dsa import _lib
+    S1, S2 = 24, 4100
+    inp = inputs.indexer_fp8(B=1, S1=S1, S2=S2, seed=77)
+    d = {k: v.to(gpu) for k, v in inp.items()}
+    ng = (S2 + 15) // 16
+    logits = torch.empty((S1, S2), device=gpu)
+    rl = torch.empty((S1,), dtype=torch.int32, device=gpu)
+    gm = torch.full((S1, ng), float("nan"), device=gpu)
+    print("indexer group maxima", flush=True)
+    _lib.check(_lib.lib().dsa_indexer_logits_fp8_group_max(
+        d["q"].data_ptr(), d["k"].data_ptr(), d["key_scale"].data_ptr(), d["w"].data_ptr(), None, None, 1, S1, S2,
+        64, 128, 3, logits.data_ptr(), S2, rl.data_ptr(), gm.data_ptr(), ng,
+        torch.cuda.current_stream().cuda_stream), "group max")
+    torch.cuda.synchronize()
+    lg, gm, rl = logits.cpu(), gm.cpu(), rl.cpu()
+    for t in range(S1):
+        L = int(rl[t])
+        row = torch.full((ng * 16,), float("-inf"))
+        row[:L] = lg[t, :L]
+        want = row.view(ng, 16).amax(dim=1)
+        n = (L + 15) // 16
+        assert torch.equal(gm[t, :n], want[:n]), t
+
+
+def test_varlen_long_rows_use_group_maxima(gpu):
+    # TND rows over prefix-summed keys long enough (>= 2 K groups of 16) for the
+    # fused selection; indices equal the stable top-k of the GPU's own logits
+    lens_q, lens_k, K = [3, 2], [70000, 66000], 2048
+    q, k, w, ks = _ragged_fp8(91, lens_q, lens_k)
+    cq, ck = _cum(lens_q), _cum(lens_k)
+    print("indexer varlen long rows", flush=True)
+    idx, vals, logits = dsa.lightning_indexer(q.to(gpu), k.to(gpu), w.to(gpu), key_scale=ks.to(gpu),
+                                              actual_seq_lengths_query=cq.to(gpu), actual_seq_lengths_key=ck.to(gpu),
+                                              layout_query="TND", layout_key="TND", sparse_count=K, sparse_mode=3,
+                                              return_value=True, return_logits=True)
+    torch.cuda.synchronize()
+    logits, idx, vals = logits.cpu(), idx.cpu(), vals.cpu()
+    row = 0
+    for b, (aq, ak) in enumerate(zip(lens_q, lens_k)):
+        for t in range(aq):
+            n = ak - aq + t + 1
+            ti, tv = stable_topk(logits[row, :n].unsqueeze(0), K)
+            assert torch.equal(idx[row, 0], ti[0]) and torch.equal(vals[row, 0], tv[0]), (b, t)
+            row += 1
