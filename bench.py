@@ -273,15 +273,16 @@ def target_configs(L, steps: int) -> dict:
 def block_sparse_indexer_configs(L, steps: int) -> dict:
     """Block-sparse indexer logits (examples/HISA/paged_block_sparse_mqa_attn_expert.py):
     the reference test's defaults (batch 1, one token, 32 heads x 128, 128-key blocks,
-    top-64 blocks of a 1024-block cache) and a decode batch of 64 tokens with the
-    same shapes; HBM bound: 256 B per key read + 4 B per logit written."""
+    top-64 blocks of a 1024-block cache), and batches of 64 and 512 tokens with the
+    same shapes; HBM bound: 256 B per key read + 4 B per logit written (algorithmic
+    bytes: tokens that pick the same block read it again, from L2 or HBM)."""
     import torch
 
     dev = torch.device("cuda:0")
     st = torch.cuda.current_stream(dev).cuda_stream
     res = {}
     g = torch.Generator(device=dev).manual_seed(8)
-    for name, batch in (("reference_default", 1), ("decode_b64", 64)):
+    for name, batch in (("reference_default", 1), ("decode_b64", 64), ("tokens_512", 512)):
         H, bs, topk, nb = 32, 128, 64, 1024
         q = torch.rand((batch, H, 128), generator=g, device=dev).half()
         kv = torch.rand((nb, bs, 1, 128), generator=g, device=dev).half()

@@ -31,12 +31,20 @@ def _case(seed, batch, seq_len, heads, bs, topk, nblocks, max_blocks, dtype):
     (4, 2, 32, 128, 16, torch.float16),
     (2, 3, 64, 64, 8, torch.bfloat16),
     (3, 1, 16, 32, 12, torch.float16),
+    # grids of >= 256 workgroups group a token's blocks four (or two) to a
+    # workgroup: ragged last groups, and 256-key blocks (two tile rounds per wave)
+    (64, 1, 32, 128, 13, torch.float16),
+    (40, 1, 16, 64, 13, torch.bfloat16),
+    (16, 4, 16, 256, 16, torch.float16),
 ])
 def test_matches_reference(gpu, batch, seq_len, heads, bs, topk, dtype):
     nblocks, max_blocks = 64, 64
     q, kv, w, ctx, bt, idx = _case(batch * 100 + heads, batch, seq_len, heads, bs, topk, nblocks, max_blocks, dtype)
     print(f"block-sparse logits B={batch} S={seq_len} H={heads} bs={bs} topk={topk} {dtype}", flush=True)
-    kern = dsa.paged_block_sparse_mqa_attn_return_logits(batch, seq_len, nblocks, bs, topk, heads, 128, max_blocks)
+    # the reference factory takes top-k counts divisible by 4 (:70); the direct
+    # entry any count
+    kern = (dsa.paged_block_sparse_mqa_attn_return_logits(batch, seq_len, nblocks, bs, topk, heads, 128, max_blocks)
+            if topk % 4 == 0 else dsa.block_sparse_indexer_logits)
     T = batch * seq_len
     got = kern(q.view(T, heads, 128).to(gpu), kv.to(gpu), idx.view(T, topk).to(gpu), w.view(T, heads).to(gpu),
                ctx.to(gpu), bt.to(gpu))

@@ -7,8 +7,10 @@
 // ref_paged_block_sparse_mqa_attn :425-468).  fp16 or bf16 q / keys / weights,
 // fp32 accumulation and output.
 //
-// One workgroup (4 waves) per (token, block); wave w takes the block's 16-key
-// tiles w, w + 4, ...  Per tile and 16-head group, four v_mfma_f32_16x16x32
+// One workgroup (4 waves) per token and up to four of its blocks (fewer when the
+// grid would drop under 256 workgroups); wave w takes each
+// block's 16-key tiles w, w + 4, ... and loads its keys of the next block before
+// scoring the current one.  Per tile and 16-head group, four v_mfma_f32_16x16x32
 // (A = q rows of 16 heads, B = K^T of 16 keys, K = 128 dims) leave lane (g, c)
 // with heads 4g .. 4g + 3 of key c; ReLU * w is summed over the lane's heads and
 // head groups, then over the four lane groups with permlane swaps.  Keys are
@@ -34,6 +36,7 @@ struct BsParams {
   float* out;               // [T, topk, bs]
   int64_t num_blocks;
   int seq_len, topk, bs, max_blocks;
+  int spg;                  // blocks of one token per workgroup (1, 2 or 4)
 };
 
 template <bool BF16>
@@ -53,22 +56,17 @@ __device__ __forceinline__ dsa::f32x4 mfma(const dsa::i32x4& a, const dsa::i32x4
 
 template <int HG, bool BF16>
 __global__ __launch_bounds__(kWaves * 64) void block_sparse_indexer_kernel(BsParams p) {
-  const int64_t item = blockIdx.x;  // (token, block slot)
-  const int64_t t = item / p.topk;
-  const int slot = (int)(item % p.topk);
+  // workgroup -> (token, up to spg consecutive block slots); a wave's keys of the
+  // next block are loaded before the current block is scored
+  const int ngroups = (p.topk + p.spg - 1) / p.spg;
+  const int64_t t = blockIdx.x / ngroups;
+  const int slot0 = (int)(blockIdx.x % ngroups) * p.spg;
+  const int nslots = min(p.spg, p.topk - slot0);
   const int b = (int)(t / p.seq_len);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
-
-  float* orow = p.out + item * p.bs;
-  const int lb = p.blk[item];
-  const int page = (lb >= 0 && lb < p.max_blocks) ? p.bt[(int64_t)b * p.max_blocks + lb] : -1;
-  const int ctx = p.ctx[b];
   const int ntiles = p.bs >> 4;
-  if (page < 0 || page >= p.num_blocks) {  // no such block: nothing is visible
-    for (int j = threadIdx.x; j < p.bs; j += kWaves * 64) orow[j] = -__builtin_inff();
-    return;
-  }
+  const int ctx = p.ctx[b];
 
   // q rows (A operands): head group hg, k-step ks -> head 16 hg + c, dims 32 ks + 8 g .. + 7
   dsa::i32x4 qa[HG][4];
@@ -83,22 +81,37 @@ __global__ __launch_bounds__(kWaves * 64) void block_sparse_indexer_kernel(BsPar
     for (int r = 0; r < 4; ++r) wv[hg][r] = to_f32<BF16>(p.w[t * (16 * HG) + 16 * hg + 4 * g + r]);
   }
 
-  const uint16_t* kb = p.kv + (int64_t)page * p.bs * kDim;
-  // two tiles per pass: the second tile's keys are loaded before the first is used
-  for (int kt0 = wave; kt0 < ntiles; kt0 += 2 * kWaves) {
-    dsa::i32x4 kf[2][4];
+  // page of slot i (-1: no such block)
+  auto page_of = [&](int i, int& lb) {
+    lb = p.blk[t * p.topk + slot0 + i];
+    const int pg = (lb >= 0 && lb < p.max_blocks) ? p.bt[(int64_t)b * p.max_blocks + lb] : -1;
+    return (pg >= 0 && pg < p.num_blocks) ? pg : -1;
+  };
+  // this wave's tiles of a block: kt = wave + kWaves u, u < kTiles (bs <= 16 kWaves kTiles is
+  // handled by the outer loop below)
+  constexpr int kTiles = 2;
+  auto load = [&](dsa::i32x4 (&kf)[kTiles][4], int pg, int kt0) {
+    const uint16_t* kb = p.kv + (int64_t)(pg < 0 ? 0 : pg) * p.bs * kDim;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kTiles; ++u) {
       const int kt = kt0 + u * kWaves;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)  // B operands: key 16 kt + c, dims 32 ks + 8 g .. + 7
-        kf[u][ks] = kt < ntiles ? *reinterpret_cast<const dsa::i32x4*>(kb + (16 * kt + c) * kDim + 32 * ks + 8 * g)
-                                : dsa::i32x4{0, 0, 0, 0};
+        kf[u][ks] = (pg >= 0 && kt < ntiles)
+                        ? *reinterpret_cast<const dsa::i32x4*>(kb + (16 * kt + c) * kDim + 32 * ks + 8 * g)
+                        : dsa::i32x4{0, 0, 0, 0};
     }
+  };
+  auto score = [&](const dsa::i32x4 (&kf)[kTiles][4], int pg, int lb, int kt0, float* orow) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kTiles; ++u) {
       const int kt = kt0 + u * kWaves;
       if (kt >= ntiles) break;  // wave-uniform
+      const int key = 16 * kt + c;
+      if (pg < 0) {
+        if (g == 0) orow[key] = -__builtin_inff();
+        continue;
+      }
       float acc = 0.f;
 #pragma unroll
       for (int hg = 0; hg < HG; ++hg) {
@@ -109,18 +122,42 @@ __global__ __launch_bounds__(kWaves * 64) void block_sparse_indexer_kernel(BsPar
         for (int r = 0; r < 4; ++r) acc = fmaf(wv[hg][r], fmaxf(d[r], 0.f), acc);
       }
       acc = dsa::xor32_sum(dsa::xor16_sum(acc));
-      const int key = 16 * kt + c;
       if (g == 0) orow[key] = (int64_t)lb * p.bs + key < ctx ? acc : -__builtin_inff();
+    }
+  };
+
+  for (int kt0 = wave; kt0 < ntiles; kt0 += kWaves * kTiles) {
+    dsa::i32x4 ka[kTiles][4], kn[kTiles][4];
+    int lba, lbn;
+    int pga = page_of(0, lba);
+    load(ka, pga, kt0);
+    for (int i = 0; i < nslots; ++i) {
+      int pgn = -1;
+      lbn = 0;
+      if (i + 1 < nslots) {
+        pgn = page_of(i + 1, lbn);
+        load(kn, pgn, kt0);
+      }
+      score(ka, pga, lba, kt0, p.out + (t * p.topk + slot0 + i) * p.bs);
+      if (i + 1 < nslots) {
+#pragma unroll
+        for (int u = 0; u < kTiles; ++u)
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) ka[u][ks] = kn[u][ks];
+        pga = pgn;
+        lba = lbn;
+      }
     }
   }
 }
 
 template <int HG>
-int launch_hg(const BsParams& p, int64_t items, bool bf16, hipStream_t st) {
+int launch_hg(const BsParams& p, int64_t tokens, bool bf16, hipStream_t st) {
+  const int64_t grid = tokens * ((p.topk + p.spg - 1) / p.spg);
   if (bf16)
-    hipLaunchKernelGGL((block_sparse_indexer_kernel<HG, true>), dim3((unsigned)items), dim3(kWaves * 64), 0, st, p);
+    hipLaunchKernelGGL((block_sparse_indexer_kernel<HG, true>), dim3((unsigned)grid), dim3(kWaves * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((block_sparse_indexer_kernel<HG, false>), dim3((unsigned)items), dim3(kWaves * 64), 0, st, p);
+    hipLaunchKernelGGL((block_sparse_indexer_kernel<HG, false>), dim3((unsigned)grid), dim3(kWaves * 64), 0, st, p);
   return dsa::check_launch("dsa_block_sparse_indexer_logits");
 }
 
@@ -162,10 +199,15 @@ extern "C" int dsa_block_sparse_indexer_logits(const void* q, const void* kv_cac
   p.bs = kv_block_size;
   p.max_blocks = max_blocks;
   hipStream_t st = (hipStream_t)stream;
+  const int64_t tokens = batch * seq_len;
+  // four blocks per workgroup unless that leaves fewer than 256 workgroups (one
+  // token's 64 blocks: 4.5 us as 64 workgroups, 8.7 us as 16)
+  p.spg = 1;
+  while (p.spg < 4 && tokens * ((topk + 2 * p.spg - 1) / (2 * p.spg)) >= 256) p.spg *= 2;
   switch (heads / 16) {
-    case 1: return launch_hg<1>(p, items, is_bf16 != 0, st);
-    case 2: return launch_hg<2>(p, items, is_bf16 != 0, st);
-    case 3: return launch_hg<3>(p, items, is_bf16 != 0, st);
-    default: return launch_hg<4>(p, items, is_bf16 != 0, st);
+    case 1: return launch_hg<1>(p, tokens, is_bf16 != 0, st);
+    case 2: return launch_hg<2>(p, tokens, is_bf16 != 0, st);
+    case 3: return launch_hg<3>(p, tokens, is_bf16 != 0, st);
+    default: return launch_hg<4>(p, tokens, is_bf16 != 0, st);
   }
 }
