@@ -159,3 +159,12 @@ def test_python_layer_rejects_bad_arguments():
     with pytest.raises(ValueError, match="d_qk"):
         dsa.sparse_mla_fwd(torch.zeros(1, 2, 16, 640, dtype=bf), torch.zeros(1, 8, 1, 640, dtype=bf),
                            torch.zeros(1, 2, 1, 4, dtype=torch.int32))
+    with pytest.raises(ValueError, match="kv_states"):
+        dsa.sparse_attn(torch.zeros(1, 2, 16, 512, dtype=bf), torch.zeros(1, 8, 256, dtype=bf),
+                        torch.zeros(16), torch.zeros(1, 2, 4, dtype=torch.int32), 0.1)
+    with pytest.raises(ValueError, match="attn_sink"):
+        dsa.sparse_attn_kernel(h=16, d=512)(torch.zeros(1, 2, 16, 512, dtype=bf), torch.zeros(1, 8, 512, dtype=bf),
+                                            torch.zeros(8), torch.zeros(1, 2, 4, dtype=torch.int32))
+    with pytest.raises(NotImplementedError, match="d = 512"):
+        dsa.sparse_attn(torch.zeros(1, 2, 16, 256, dtype=bf), torch.zeros(1, 8, 256, dtype=bf),
+                        torch.zeros(16), torch.zeros(1, 2, 4, dtype=torch.int32), 0.1)

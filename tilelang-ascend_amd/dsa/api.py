@@ -441,6 +441,46 @@ def sparse_attention_fwd(heads: int, dim: int, tail_dim: int, topk: int, kv_stri
     return kernel
 
 
+def sparse_attn(query_states: torch.Tensor, kv_states: torch.Tensor, attn_sink: torch.Tensor,
+                topk_idxs: torch.Tensor, softmax_scale: float) -> torch.Tensor:
+    """DeepSeek-V4 sparse attention with a per-head sink, on the sparse MLA core
+    (examples/deepseek_v4/sparse_attention.py:171-198 for the semantics, kernel
+    :27-168): q ``[b, m, h, d]`` bf16, kv ``[b, n, d]`` bf16 (K = V, d = 512),
+    attn_sink ``[h]`` fp32, topk_idxs ``[b, m, topk]`` int32 -> fp32 ``[b, m, h, d]``.
+    ``-1`` (and out-of-range) indices select nothing; no causal rule.  The core
+    rounds P and the output to bf16 (the output is returned widened to fp32)."""
+    if query_states.dim() != 4 or kv_states.dim() != 3 or topk_idxs.dim() != 3:
+        raise ValueError("query_states must be [b, m, h, d], kv_states [b, n, d] and topk_idxs [b, m, topk]")
+    b, m, h, d = query_states.shape
+    if kv_states.shape[0] != b or kv_states.shape[2] != d:
+        raise ValueError(f"kv_states must be [{b}, n, {d}], got {tuple(kv_states.shape)}")
+    if tuple(topk_idxs.shape[:2]) != (b, m):
+        raise ValueError(f"topk_idxs must be [{b}, {m}, topk], got {tuple(topk_idxs.shape)}")
+    if d != 512:
+        raise NotImplementedError(f"d = 512 only (got {d})")
+    _require_gpu(query_states, kv_states, topk_idxs)
+    _require_contiguous("kv_states", kv_states)
+    _require_contiguous("topk_idxs", topk_idxs)
+    out = sparse_mla_fwd(query_states.contiguous(), kv_states.unsqueeze(2), topk_idxs.unsqueeze(2),
+                         float(softmax_scale), is_causal=False, attn_sink=attn_sink, return_lse=False)
+    return out.float()
+
+
+def sparse_attn_kernel(h: int, d: int, scale: Optional[float] = None) -> Callable:
+    """Factory with the signature of the reference's ``sparse_attn_kernel``
+    (examples/deepseek_v4/sparse_attention.py:27-34, ``out_idx=[2]``): returns
+    ``kernel(q, kv, attn_sink, topk_idxs) -> output`` fp32 ``[b, m, h, d]``;
+    ``scale`` defaults to ``d ** -0.5`` as there (:34)."""
+    sc = (1.0 / d) ** 0.5 if scale is None else scale
+
+    def kernel(q: torch.Tensor, kv: torch.Tensor, attn_sink: torch.Tensor, topk_idxs: torch.Tensor) -> torch.Tensor:
+        if q.dim() != 4 or q.shape[2] != h or q.shape[3] != d or attn_sink.numel() != h:
+            raise ValueError(f"q must be [b, m, {h}, {d}] and attn_sink [{h}]")
+        return sparse_attn(q, kv, attn_sink, topk_idxs, sc)
+
+    return kernel
+
+
 # ---------------------------------------------------------------------------
 # row quantisation (the producer of the indexer's fp8 operands; int8 act quant)
 # ---------------------------------------------------------------------------
