@@ -130,3 +130,34 @@ def test_paged_prefill_per_batch_lengths(gpu, block_size):
                                        q_start_index_s=kv_len[b] - S, is_causal=True, p_dtype=torch.bfloat16)
         torch.testing.assert_close(out[b:b + 1].float().cpu(), ro, **OUT_TOL)
         torch.testing.assert_close(lse[b:b + 1].cpu(), rl, **LSE_TOL)
+
+
+@pytest.mark.parametrize("rope,T,act_q", [(True, 3, 3), (True, 4, 3), (False, 2, 2)])
+def test_sparse_attn_tilelang_signature(gpu, rope, T, act_q):
+    # bench_sfa.py:9-56 recipe: TND query, PA_BSND key (value = key), N(0, 0.5)
+    # inputs, indices = topk of uniform noise over the first act_kv_s keys, an identity
+    # block table, scale 0.5; rows past actual_seq_lengths_query are zero here
+    g = torch.Generator().manual_seed(40 + T)
+    N, D, Dr, bs, KV_S, act_kv, topk = 128, 512, 64, 128, 6400, 2560, 2048
+    query = (torch.randn((T, N, D), generator=g) * 0.5).bfloat16()
+    key = (torch.randn((KV_S // bs, bs, 1, D), generator=g) * 0.5).bfloat16()
+    qr = (torch.randn((T, N, Dr), generator=g) * 0.5).bfloat16() if rope else None
+    kr = (torch.randn((KV_S // bs, bs, 1, Dr), generator=g) * 0.5).bfloat16() if rope else None
+    idx = torch.topk(torch.rand((T, 1, act_kv), generator=g), topk, dim=-1).indices.int()
+    bt = torch.arange(KV_S // bs, dtype=torch.int32).view(1, -1)
+    aq, ak = torch.tensor([act_q], dtype=torch.int32), torch.tensor([act_kv], dtype=torch.int32)
+    print(f"sparse_attn_tilelang rope={rope} T={T} act_q={act_q}", flush=True)
+    dv = lambda t: None if t is None else t.to(gpu)
+    out = dsa.sparse_attn_tilelang(query=dv(query), key=dv(key), value=dv(key), sparse_indices=dv(idx),
+                                   scale_value=0.5, sparse_block_size=1, actual_seq_lengths_query=dv(aq),
+                                   actual_seq_lengths_kv=dv(ak), query_rope=dv(qr), key_rope=dv(kr),
+                                   layout_query="TND", layout_kv="PA_BSND", sparse_mode=0, block_table=dv(bt),
+                                   attention_mode=2)
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (T, N, D) and out.dtype == torch.bfloat16
+    q = torch.cat((query, qr), -1) if rope else query
+    kv = torch.cat((key, kr), -1) if rope else key
+    ro, _ = sparse_mla_fwd_gather(q[:act_q].unsqueeze(0), kv, idx[:act_q].unsqueeze(0), 0.5, block_table=bt,
+                                  q_start_index_s=act_kv - act_q, is_causal=True, p_dtype=torch.bfloat16)
+    torch.testing.assert_close(out[:act_q].float().cpu(), ro[0], **OUT_TOL)
+    assert not out[act_q:].any()

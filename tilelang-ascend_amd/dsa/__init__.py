@@ -17,6 +17,7 @@ from .api import (  # noqa: F401
     simple_topk_selector,
     sparse_attention_fwd,
     sparse_attn,
+    sparse_attn_tilelang,
     sparse_attn_kernel,
     sparse_flash_mla,
     sparse_mla_fwd,
@@ -26,7 +27,7 @@ from ._lib import DSAError, LIB_PATH, lib  # noqa: F401
 
 __all__ = [
     "lightning_indexer", "indexer_logits", "topk_selector", "simple_topk_selector",
-    "sparse_mla_fwd", "sparse_attention_fwd", "sparse_attn", "sparse_attn_kernel", "act_quant", "act_quant_kernel_int8_optimized",
+    "sparse_mla_fwd", "sparse_attention_fwd", "sparse_attn", "sparse_attn_kernel", "sparse_attn_tilelang", "act_quant", "act_quant_kernel_int8_optimized",
     "sparse_flash_mla", "block_sparse_indexer_logits", "paged_block_sparse_mqa_attn_return_logits", "quant_fp8", "paged_slots", "indexer_k_append_fp8", "indexer_q_quant_fp8",
     "DSAError", "LIB_PATH", "lib",
 ]

@@ -441,6 +441,58 @@ def sparse_attention_fwd(heads: int, dim: int, tail_dim: int, topk: int, kv_stri
     return kernel
 
 
+def sparse_attn_tilelang(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, sparse_indices: torch.Tensor,
+                         scale_value: float, sparse_block_size: int, actual_seq_lengths_query: torch.Tensor,
+                         actual_seq_lengths_kv: torch.Tensor, query_rope: Optional[torch.Tensor] = None,
+                         key_rope: Optional[torch.Tensor] = None, layout_query: str = "BSND",
+                         layout_kv: str = "BSND", sparse_mode: int = 3, block_table: Optional[torch.Tensor] = None,
+                         attention_mode=None) -> torch.Tensor:
+    """Paged sparse MLA with the signature of the reference's ``sparse_attn_tilelang``
+    (examples/sparse_flash_attention/bench_sfa/sparse_flash_attn_pa_no_cv_pipeline.py:384-419,
+    the ``npu_sparse_flash_attention`` argument list of bench_sfa.py:55-73).
+
+    query ``[T, N, 512]`` (TND, one batch: the reference views it as ``[1, T, N, D]``),
+    key ``[blocks, block_size, 1, 512]`` (PA_BSND, ``value`` is the same cache and is
+    not read, as there), query_rope ``[T, N, 64]`` / key_rope ``[blocks, block_size, 1, 64]``
+    or both None, sparse_indices ``[T, 1, topk]`` int32, block_table ``[1, max_blocks]``.
+    Row s attends to its indices ``<= actual_seq_lengths_kv[0] - actual_seq_lengths_query[0] + s``
+    (the kernel's rule, :185, applied for sparse_mode 0 and 3 alike); rows
+    ``s >= actual_seq_lengths_query[0]`` are not computed there and are zero here.
+    Returns ``[T, N, 512]`` bf16.  With rope parts the key cache is joined into one
+    ``[blocks, block_size, 1, 576]`` copy per call, as the reference does (:406);
+    callers that keep a joined cache call ``sparse_mla_fwd`` on it directly."""
+    if sparse_block_size != 1:
+        raise ValueError(f"sparse_block_size must be 1, got {sparse_block_size}")
+    if sparse_mode not in (0, 3):
+        raise ValueError(f"sparse_mode must be 0 or 3, got {sparse_mode}")
+    if query.dim() != 3 or key.dim() != 4 or key.shape[2] != 1:
+        raise ValueError("query must be [T, N, D] and key [blocks, block_size, 1, D]")
+    if block_table is None or block_table.dim() != 2:
+        raise ValueError("block_table [batch, max_blocks] is required")
+    if (query_rope is None) != (key_rope is None):
+        raise ValueError("query_rope and key_rope are given together or not at all")
+    if block_table.shape[0] != 1 or actual_seq_lengths_query.numel() != 1 or actual_seq_lengths_kv.numel() != 1:
+        raise NotImplementedError("one batch, as the reference wrapper (query.unsqueeze(0))")
+    T, N, D = query.shape
+    if sparse_indices.dim() != 3 or sparse_indices.shape[0] != T or sparse_indices.shape[1] != 1:
+        raise ValueError(f"sparse_indices must be [{T}, 1, topk], got {tuple(sparse_indices.shape)}")
+    dev = _require_gpu(query, key)
+    if query_rope is not None:
+        q = torch.cat((query, query_rope.to(query.dtype)), dim=-1).unsqueeze(0).contiguous()
+        kv = torch.cat((key, key_rope.to(key.dtype)), dim=-1).contiguous()
+    else:
+        q = query.unsqueeze(0).contiguous()
+        kv = key.contiguous()
+    act_q = int(actual_seq_lengths_query.reshape(-1)[0])
+    act_kv = actual_seq_lengths_kv.reshape(1).to(device=dev, dtype=torch.int32)
+    idx = sparse_indices.to(device=dev, dtype=torch.int32).contiguous().view(1, T, 1, -1)
+    out = sparse_mla_fwd(q, kv, idx, float(scale_value), block_table=block_table, seq_len_kv=act_kv,
+                         q_start_index_s=act_kv - act_q, is_causal=True, return_lse=False)[0]
+    if act_q < T:
+        out[max(act_q, 0):].zero_()
+    return out
+
+
 def sparse_attn(query_states: torch.Tensor, kv_states: torch.Tensor, attn_sink: torch.Tensor,
                 topk_idxs: torch.Tensor, softmax_scale: float) -> torch.Tensor:
     """DeepSeek-V4 sparse attention with a per-head sink, on the sparse MLA core
