@@ -433,62 +433,68 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
 }
 
 // Merge split partials: lse = logsumexp_p lse_p, out = sum_p exp(lse_p - lse) out_p.
-// One 128-thread group per (token, head); each thread owns 4 consecutive dims.
+// 64 threads per (token, head) row, 8 dims (16 bytes of fp16) each, four rows per
+// block.  The lse, scale and slice of kCombineU splits are all loaded before any
+// is used, so a row costs one round trip per kCombineU splits; chunks beyond the
+// first are merged online (the running sums rescaled to the new maximum).
+constexpr int kCombineU = 8;
+constexpr int kCombineRows = 4;  // rows per 256-thread block
+
 __global__ __launch_bounds__(256) void mla_combine_kernel(const uint16_t* __restrict__ part_o,
                                                           const float* __restrict__ part_lse,
                                                           const float* __restrict__ part_scale,
                                                           int64_t rows, int H, int nsplit,
                                                           uint16_t* __restrict__ out,
                                                           float* __restrict__ lse) {
-  const int64_t rh = (int64_t)blockIdx.x * 2 + (threadIdx.x >> 7);
+  const int64_t rh = (int64_t)blockIdx.x * kCombineRows + (threadIdx.x >> 6);
   if (rh >= rows) return;
-  const int d4 = threadIdx.x & 127;
+  const int d8 = threadIdx.x & 63;
   const int64_t token = rh / H;
   const int head = (int)(rh % H);
-  // up to kU splits per batch: their loads are all issued before any is used
-  constexpr int kU = 8;
-  float mx = -__builtin_inff();
-  for (int sp0 = 0; sp0 < nsplit; sp0 += kU) {
-    float l[kU];
+  const int64_t row0 = token * nsplit * H + head;  // partial row of split 0
+  float mx = -__builtin_inff(), den = 0.f;
+  float acc[8];
 #pragma unroll
-    for (int u = 0; u < kU; ++u)
-      l[u] = sp0 + u < nsplit ? part_lse[(token * nsplit + sp0 + u) * H + head] : -__builtin_inff();
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += kCombineU) {
+    float l[kCombineU], sc[kCombineU];
+    dsa::i32x4 v[kCombineU];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) mx = fmaxf(mx, l[u]);
-  }
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  float den = 0.f;
-  if (mx != -__builtin_inff()) {
-    for (int sp0 = 0; sp0 < nsplit; sp0 += kU) {
-      float l[kU], sc[kU];
-      dsa::i32x2 v[kU];
+    for (int u = 0; u < kCombineU; ++u) {
+      const bool ok = s0 + u < nsplit;
+      const int64_t prow = row0 + (int64_t)(s0 + u) * H;
+      l[u] = ok ? part_lse[prow] : -__builtin_inff();
+      sc[u] = ok ? part_scale[prow] : 0.f;
+      v[u] = ok ? *reinterpret_cast<const dsa::i32x4*>(part_o + prow * kDV + 8 * d8) : dsa::i32x4{0, 0, 0, 0};
+    }
+    float cm = mx;
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const bool ok = sp0 + u < nsplit;
-        const int64_t prow = (token * nsplit + sp0 + u) * H + head;
-        l[u] = ok ? part_lse[prow] : -__builtin_inff();
-        sc[u] = ok ? part_scale[prow] : 0.f;
-        v[u] = ok ? *reinterpret_cast<const dsa::i32x2*>(part_o + prow * kDV + 4 * d4) : dsa::i32x2{0, 0};
-      }
+    for (int u = 0; u < kCombineU; ++u) cm = fmaxf(cm, l[u]);
+    if (cm == -__builtin_inff()) continue;  // nothing valid so far
+    const float r = mx == -__builtin_inff() ? 0.f : __expf(mx - cm);
+    den *= r;
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const float wgt = l[u] == -__builtin_inff() ? 0.f : __expf(l[u] - mx);
-        den += wgt;
-        const float ws = wgt * sc[u];
-        const uint32_t w0 = (uint32_t)v[u][0], w1 = (uint32_t)v[u][1];
-        acc[0] += ws * (float)__builtin_bit_cast(_Float16, (uint16_t)(w0 & 0xffffu));
-        acc[1] += ws * (float)__builtin_bit_cast(_Float16, (uint16_t)(w0 >> 16));
-        acc[2] += ws * (float)__builtin_bit_cast(_Float16, (uint16_t)(w1 & 0xffffu));
-        acc[3] += ws * (float)__builtin_bit_cast(_Float16, (uint16_t)(w1 >> 16));
+    for (int e = 0; e < 8; ++e) acc[e] *= r;
+#pragma unroll
+    for (int u = 0; u < kCombineU; ++u) {
+      const float w = l[u] == -__builtin_inff() ? 0.f : __expf(l[u] - cm);
+      den += w;
+      const float ws = w * sc[u];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t w2 = (uint32_t)v[u][e >> 1];
+        const uint16_t h = (uint16_t)((e & 1) ? (w2 >> 16) : (w2 & 0xffffu));
+        acc[e] = fmaf(ws, (float)__builtin_bit_cast(_Float16, h), acc[e]);
       }
     }
+    mx = cm;
   }
-  const float inv = den > 0.f ? 1.f / den : 0.f;
-  dsa::i32x2 v;
-  v[0] = (int)dsa::pack_bf16x2(acc[0] * inv, acc[1] * inv);
-  v[1] = (int)dsa::pack_bf16x2(acc[2] * inv, acc[3] * inv);
-  *reinterpret_cast<dsa::i32x2*>(out + rh * kDV + 4 * d4) = v;
-  if (d4 == 0 && lse) lse[rh] = den > 0.f ? mx + __logf(den) : -__builtin_inff();
+  const float f = den > 0.f ? 1.f / den : 0.f;
+  dsa::i32x4 ov;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) ov[e] = (int)dsa::pack_bf16x2(acc[2 * e] * f, acc[2 * e + 1] * f);
+  *reinterpret_cast<dsa::i32x4*>(out + rh * kDV + 8 * d8) = ov;
+  if (d8 == 0 && lse) lse[rh] = den > 0.f ? mx + __logf(den) : -__builtin_inff();
 }
 
 template <int DQK, int STAGES>
@@ -613,7 +619,7 @@ int sparse_mla_run(const MlaRun& r, const char* what) {
   const int rc = r.d_qk == 576 ? launch_mla<576>(p, nblocks, st) : launch_mla<512>(p, nblocks, st);
   if (rc != kOk || ns == 1) return rc;
   const int64_t rows = T * r.H;
-  hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, st,
+  hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)((rows + kCombineRows - 1) / kCombineRows)), dim3(256), 0, st,
                      p.part_o, p.part_lse, p.part_scale, rows, r.H, ns, p.out, r.lse);
   return check_launch("dsa_sparse_mla_fwd(combine)");
 }
