@@ -487,10 +487,13 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
   p.S2 = S2;
   p.sparse_mode = sparse_mode;
   p.ntb = (S1 + kTokPerBlock - 1) / kTokPerBlock;
-  // Aim for >= 4 workgroups per CU over the whole launch while keeping each
-  // workgroup's key chunk a multiple of the LDS tile.
+  // Shrink the key chunk (a multiple of the LDS tile) until the launch has one
+  // workgroup per CU.  A workgroup's fixed cost (A operands, ring fill, the
+  // group-maxima flush) is worth amortising over a longer chunk: with 32 query
+  // rows x 128K keys, 256 workgroups of 1024 keys take 39 us where 1024 of 256
+  // keys took 70.
   int chunk = kMaxChunk;
-  while (chunk > kKeyTile && (int64_t)B * p.ntb * ((S2 + chunk - 1) / chunk) < 1024) chunk >>= 1;
+  while (chunk > kKeyTile && (int64_t)B * p.ntb * ((S2 + chunk - 1) / chunk) < 256) chunk >>= 1;
   p.chunk = chunk;
   p.nkc = (S2 + chunk - 1) / chunk;
   const int64_t groups = (int64_t)B * p.nkc;
