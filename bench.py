@@ -260,6 +260,7 @@ def target_configs(L, steps: int) -> dict:
     qbytes = qb.numel() * 3 + wq.numel() * 8
     del kb, k8, ks, qb, wq, q8, wo
     torch.cuda.empty_cache()
+    res["indexer_decode"] = indexer_decode_configs(L, steps)
     res["flash_mla_v4"] = flash_mla_v4_configs(L, steps)
     res["block_sparse_indexer"] = block_sparse_indexer_configs(L, steps)
     res["fp8_producers"] = {"key_cache_128k_us": round(uk, 2),
@@ -268,6 +269,37 @@ def target_configs(L, steps: int) -> dict:
                             "query_frac_of_hbm": round(qbytes / uq / 1e3 / PEAK_HBM_GBS, 4),
                             "algorithmic_bytes": {"key_cache": kbytes, "query": qbytes}}
     return res
+
+
+def indexer_decode_configs(L, steps: int) -> dict:
+    """Indexer logits for a decode batch: 32 sequences x one query row x 128K keys
+    each (distinct key caches, 553 MB of fp8 keys + scales), the indexer's decode
+    form; HBM bound (132 B per key read once, 4 B per logit written)."""
+    import torch
+
+    from dsa import inputs
+
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream(dev).cuda_stream
+    B, S2 = 32, 131072
+    ix = inputs.indexer_fp8(B=B, S1=1, S2=S2, seed=9, device=dev)
+    lg = torch.empty((B, S2), device=dev)
+    rl = torch.empty((B,), dtype=torch.int32, device=dev)
+    gm = torch.empty((B, S2 // 16), device=dev)
+
+    def run():
+        rc = L.dsa_indexer_logits_fp8_group_max(ix["q"].data_ptr(), ix["k"].data_ptr(), ix["key_scale"].data_ptr(),
+                                                ix["w"].data_ptr(), None, None, B, 1, S2, IDX_HEADS, IDX_DIM, 0,
+                                                lg.data_ptr(), S2, rl.data_ptr(), gm.data_ptr(), S2 // 16, st)
+        if rc != 0:
+            raise RuntimeError(L.dsa_last_error().decode())
+
+    us = _time_launches(run, steps)
+    byts = B * S2 * (IDX_DIM + 4 + 4) + B * S2 // 16 * 4
+    del ix, lg, rl, gm
+    torch.cuda.empty_cache()
+    return {"b32_128k_distinct_us": round(us, 1), "gbs": round(byts / us / 1e3, 1),
+            "frac_of_hbm": round(byts / us / 1e3 / PEAK_HBM_GBS, 4), "algorithmic_bytes": byts}
 
 
 def block_sparse_indexer_configs(L, steps: int) -> dict:

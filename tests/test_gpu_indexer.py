@@ -310,3 +310,77 @@ def test_varlen_long_rows_use_group_maxima(gpu):
             ti, tv = stable_topk(logits[row, :n].unsqueeze(0), K)
             assert torch.equal(idx[row, 0], ti[0]) and torch.equal(vals[row, 0], tv[0]), (b, t)
             row += 1
+
+
+# ---- the decode form (batch rows of at most 4 query tokens: one wave per token
+# and key chunk, keys loaded straight into registers)
+@pytest.mark.parametrize("B,S1,S2,mode,scaled", [(8, 1, 9000, 0, True), (8, 1, 9000, 3, False),
+                                                  (2, 4, 5000, 3, True), (3, 2, 700, 0, True)])
+def test_decode_form(gpu, B, S1, S2, mode, scaled):
+    from dsa import _lib
+    inp = inputs.indexer_fp8(B=B, S1=S1, S2=S2, seed=B * 100 + S1 + mode)
+    act_k = torch.tensor([S2 - 37 * b for b in range(B)], dtype=torch.int32)
+    act_q = torch.tensor([S1 - (b % S1) for b in range(B)], dtype=torch.int32)
+    ks = inp["key_scale"] if scaled else None
+    print(f"indexer decode form B={B} S1={S1} S2={S2} mode={mode} scaled={scaled}", flush=True)
+    d = {k: v.to(gpu) for k, v in inp.items()}
+    aq_d, ak_d = act_q.to(gpu), act_k.to(gpu)  # held: the launch reads them asynchronously
+    ng = (S2 + 15) // 16
+    logits = torch.empty((B * S1, S2), device=gpu)
+    rl = torch.full((B * S1,), -7, dtype=torch.int32, device=gpu)
+    gm = torch.empty((B * S1, ng), device=gpu)
+    _lib.check(_lib.lib().dsa_indexer_logits_fp8_group_max(
+        d["q"].data_ptr(), d["k"].data_ptr(), d["key_scale"].data_ptr() if scaled else None, d["w"].data_ptr(),
+        aq_d.data_ptr(), ak_d.data_ptr(), B, S1, S2, 64, 128, mode, logits.data_ptr(), S2,
+        rl.data_ptr(), gm.data_ptr(), ng, torch.cuda.current_stream().cuda_stream), "decode form")
+    torch.cuda.synchronize()
+    logits, rl, gm = logits.cpu(), rl.cpu(), gm.cpu()
+    _, rscores, _ = ref_indexer(inp["q"], inp["k"], inp["w"], key_scale=ks, actual_seq_lengths_query=act_q,
+                                actual_seq_lengths_key=act_k, sparse_count=64, sparse_mode=mode)
+    for b in range(B):
+        for t in range(S1):
+            r = b * S1 + t
+            ref = rscores[b, 0, t]
+            n = int(torch.isfinite(ref).sum())
+            assert int(rl[r]) == n, (b, t)  # rows past act_q: 0
+            if n == 0:
+                continue
+            _logit_close(logits[r, :n], ref[:n])
+            row = torch.full((ng * 16,), float("-inf"))
+            row[:n] = logits[r, :n]
+            m = (n + 15) // 16
+            assert torch.equal(gm[r, :m], row.view(ng, 16).amax(dim=1)[:m]), (b, t)
+
+
+def test_decode_form_shared_pool(gpu):
+    # 32 single-token rows, each through its own block table onto one shared page
+    # pool (the layer's decode step): bit-identical to the contiguous layout, and
+    # the fused top-k equals the stable top-k of the logits
+    B, S2, bs, K = 32, 20000, 64, 2048
+    inp = inputs.indexer_fp8(B=1, S1=B, S2=S2, seed=123)
+    q = inp["q"].view(B, 1, 64, 128)
+    w = inp["w"].view(B, 1, 64)
+    nb = (S2 + bs - 1) // bs
+    pool = torch.zeros((nb, bs, 1, 128), dtype=torch.uint8)
+    pool.view(-1, 128)[:S2] = inp["k"].view(torch.uint8).view(S2, 128)
+    pscale = torch.zeros((nb, bs))
+    pscale.view(-1)[:S2] = inp["key_scale"].view(-1)
+    bt = torch.arange(nb, dtype=torch.int32).repeat(B, 1)
+    kc = inp["k"].expand(B, S2, 1, 128).contiguous()
+    kscale = inp["key_scale"].expand(B, S2).contiguous()
+    print("indexer decode form, 32 rows over one shared pool", flush=True)
+    # (PA_BSND takes no return_value, lightning_indexer.py:1235-1236)
+    ip, _, lp = dsa.lightning_indexer(q.to(gpu), pool.view(inputs.FP8).to(gpu), w.to(gpu), key_scale=pscale.to(gpu),
+                                      actual_seq_lengths_key=torch.full((B,), S2, dtype=torch.int32).to(gpu),
+                                      block_table=bt.to(gpu), layout_key="PA_BSND", sparse_count=K, sparse_mode=0,
+                                      return_logits=True)
+    ic, vc, lc = dsa.lightning_indexer(q.to(gpu), kc.to(gpu), w.to(gpu), key_scale=kscale.to(gpu), sparse_count=K,
+                                       sparse_mode=0, return_value=True, return_logits=True)
+    torch.cuda.synchronize()
+    lp, lc, ip, ic, vc = lp.cpu(), lc.cpu(), ip.cpu(), ic.cpu(), vc.cpu()
+    assert torch.equal(lp, lc) and torch.equal(ip, ic)
+    ti, tv = stable_topk(lc.view(B, S2), K)
+    assert torch.equal(ic.view(B, K), ti) and torch.equal(vc.view(B, K), tv)
+    # one row against the oracle
+    _, rs, _ = ref_indexer(q[:1], kc[:1], w[:1], key_scale=kscale[:1], sparse_count=K, sparse_mode=0)
+    _logit_close(lp[0, 0], rs[0, 0, 0])

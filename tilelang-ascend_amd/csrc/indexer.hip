@@ -454,6 +454,229 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   if (loader) dsa::wait_vmcnt<0>();
 }
 
+// ---- decode form: batch rows of at most kDecMaxTok query tokens ---------------
+// The kernel above shares each LDS key tile among the 16 tokens of a workgroup;
+// with one token per batch row (decode) 15 of its 16 waves would idle.  Here every
+// wave is independent: one (batch row, token, key chunk) per wave, its token's A
+// operands and u pieces in registers, its keys loaded straight from global memory
+// into B-operand registers, two 64-key tiles in flight, no LDS ring and no
+// barriers.  Per 16-key block: the same 4 + 1 fp8 MFMAs and 16 FMAs as above, the
+// same operand bytes and the same order of additions (the u MFMA repeats the four
+// pieces in every row group, so each lane group receives u.k of the block and
+// lane 16 j + c keeps block j's), so both forms write bit-identical logits; then
+// the same reduce-scatter, key scale, mask and group maxima.
+constexpr int kDecWaves = 4;
+constexpr int kDecMaxTok = 4;
+constexpr int kDecRing = 2;  // 3 and 4 measured no faster (the stream runs at ~4.5 TB/s either way)
+constexpr int kDecMaxChunk = 2048;
+
+template <bool PAGED, bool SCALED>
+__global__ __launch_bounds__(kDecWaves * 64) void indexer_decode_kernel(IndexerParams p) {
+  __shared__ __align__(16) uint8_t upieces[kDecWaves][kSplits][kDim];
+  __shared__ int32_t drows[PAGED ? kDecWaves : 1][PAGED ? kDecMaxChunk : 1];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int64_t unit = (int64_t)blockIdx.x * kDecWaves + wave;  // (b, t, kc), kc fastest
+  if (unit >= (int64_t)p.B * p.S1 * p.nkc) return;
+  const int kc = (int)(unit % p.nkc);
+  const int t = (int)((unit / p.nkc) % p.S1);
+  const int b = (int)(unit / ((int64_t)p.nkc * p.S1));
+
+  int aq, ak;
+  int64_t qbase, kbase_row;
+  if (p.cum_q) {
+    qbase = b > 0 ? p.cum_q[b - 1] : 0;
+    aq = clampi(p.cum_q[b] - (int)qbase, 0, p.S1);
+  } else {
+    qbase = (int64_t)b * p.S1;
+    aq = p.act_q ? clampi(p.act_q[b], 0, p.S1) : p.S1;
+  }
+  if (p.cum_k) {
+    kbase_row = b > 0 ? p.cum_k[b - 1] : 0;
+    ak = clampi(p.cum_k[b] - (int)kbase_row, 0, p.S2);
+  } else {
+    kbase_row = (int64_t)b * p.S2;
+    ak = p.act_k ? clampi(p.act_k[b], 0, p.S2) : p.S2;
+  }
+  if (p.cum_q && t >= aq) return;  // varlen rows past the batch's length do not exist
+  const int L = visible_keys(t, aq, ak, p.sparse_mode);
+  const int64_t trow = qbase + t;
+  if (kc == 0 && p.row_len != nullptr && lane == 0) p.row_len[trow] = L;
+  const int k0 = kc * p.chunk;
+  const int kend = min(k0 + p.chunk, p.S2);
+  const int k1 = min(kend, L);
+  if (k0 >= k1) return;
+
+  // q: lane (g, c) holds head 16 mt + c, bytes [32g, 32g+32).
+  dsa::i32x8 qa[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const uint8_t* src = p.q + (trow * kHeads + 16 * mt + c) * kDim + 32 * g;
+    const dsa::i32x4 lo = *reinterpret_cast<const dsa::i32x4*>(src);
+    const dsa::i32x4 hi = *reinterpret_cast<const dsa::i32x4*>(src + 16);
+    qa[mt] = dsa::i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  float wh[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wh[mt][i] = 0.5f * p.w[trow * kHeads + 16 * mt + 4 * g + i];
+
+  // u/2 = sum_h (w_h / 2) q_h (lane l: dims 2l, 2l+1) and its fp8 pieces, as above.
+  float u0 = 0.f, u1 = 0.f;
+  {
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(p.q + trow * kHeads * kDim) + lane;
+    const float* wrow = p.w + trow * kHeads;
+#pragma unroll 8
+    for (int h = 0; h < kHeads; ++h) {
+      const uint32_t two = qrow[h * (kDim / 2)];
+      const float wv = 0.5f * wrow[h];
+      u0 = fmaf(wv, fp8_to_f32(two & 0xff), u0);
+      u1 = fmaf(wv, fp8_to_f32(two >> 8), u1);
+    }
+  }
+  float umax = fmaxf(fabsf(u0), fabsf(u1));
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) umax = fmaxf(umax, __shfl_xor(umax, d, 64));
+  int e = -100;
+  if (umax > 0.f) {
+    int ex;
+    (void)frexpf(umax / (float)kE4m3Max, &ex);
+    e = clampi(ex, -100, 100);
+  }
+  {
+    float r0 = u0, r1 = u1;
+#pragma unroll
+    for (int sp = 0; sp < kSplits; ++sp) {
+      const float inv = ldexpf(1.f, 4 * sp - e), sig = ldexpf(1.f, e - 4 * sp);
+      const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(r0 * inv, r1 * inv, 0, false);
+      *reinterpret_cast<uint16_t*>(&upieces[wave][sp][2 * lane]) = (uint16_t)pk;
+      r0 = fmaf(-sig, __builtin_amdgcn_cvt_f32_fp8(pk, 0), r0);
+      r1 = fmaf(-sig, __builtin_amdgcn_cvt_f32_fp8(pk, 1), r1);
+    }
+  }
+  const uint8_t* kbase = PAGED ? p.k : p.k + kbase_row * kDim;
+  const float* sbase = SCALED ? (PAGED ? p.key_scale : p.key_scale + kbase_row) : nullptr;
+  if constexpr (PAGED) {
+    for (int i = lane; i < k1 - k0; i += 64) {
+      const int key = k0 + i;
+      const int blk = key / p.block_size;
+      const int pg = blk < p.max_blocks ? p.block_table[(int64_t)b * p.max_blocks + blk] : -1;
+      const int64_t row = (int64_t)pg * p.block_size + key % p.block_size;
+      drows[wave][i] = (pg >= 0 && row < p.pool_rows) ? (int32_t)row : -1;
+    }
+  }
+  // this wave's LDS writes (u pieces, rows) are read back by other lanes of the wave
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // u pieces as A rows: row r holds piece r % 4 (scale 2^(e - 4 (r % 4))), so lane
+  // (g, c) of the result holds the four pieces of u.k for key c in every group g
+  dsa::i32x8 ua;
+  {
+    const dsa::i32x4 lo = *reinterpret_cast<const dsa::i32x4*>(&upieces[wave][c & 3][32 * g]);
+    const dsa::i32x4 hi = *reinterpret_cast<const dsa::i32x4*>(&upieces[wave][c & 3][32 * g + 16]);
+    ua = dsa::i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  const int uscale = clampi(127 + e - 4 * (c & 3), 1, 254);
+
+  auto row_of = [&](int key) -> int {  // physical row of key in [k0, k1), -1 outside the pool
+    if constexpr (PAGED) return drows[wave][key - k0];
+    else return key;
+  };
+  const int ntiles = (k1 - k0 + kKeyTile - 1) / kKeyTile;
+  dsa::i32x4 kb[kDecRing][4][2];
+  float ks[kDecRing];
+  auto issue = [&](int tile, auto SLOT) {
+    constexpr int sl = decltype(SLOT)::value;
+    const int tt = tile < ntiles ? tile : ntiles - 1;  // past the end: reload the last tile (never used)
+    const int kt0 = k0 + tt * kKeyTile;
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const int row = row_of(min(kt0 + 16 * blk + c, k1 - 1));
+      const uint8_t* src = (row >= 0 ? kbase + (int64_t)row * kDim : g_zero_key) + 32 * g;
+      kb[sl][blk][0] = *reinterpret_cast<const dsa::i32x4*>(src);
+      kb[sl][blk][1] = *reinterpret_cast<const dsa::i32x4*>(src + 16);
+    }
+    if constexpr (SCALED) {
+      const int row = row_of(min(kt0 + lane, k1 - 1));
+      ks[sl] = row >= 0 ? sbase[row] : 0.f;
+    } else {
+      ks[sl] = 1.f;
+    }
+  };
+
+  float* orow = p.logits + trow * p.ld + k0;
+  const __amdgpu_buffer_rsrc_t ost = __builtin_amdgcn_make_buffer_rsrc(orow, (short)0, (kend - k0) * 4, 0x00020000);
+  const bool want_gmax = p.gmax != nullptr;
+  const __amdgpu_buffer_rsrc_t gst = __builtin_amdgcn_make_buffer_rsrc(
+      want_gmax ? p.gmax + trow * p.ld_g + k0 / 16 : p.logits, (short)0,
+      want_gmax ? ((kend - k0 + 15) / 16) * 4 : 0, 0x00020000);
+  const dsa::f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int tile, auto SLOT) {
+    constexpr int sl = decltype(SLOT)::value;
+    float ap[4], lin = 0.f;
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const dsa::i32x8 bf = {kb[sl][blk][0][0], kb[sl][blk][0][1], kb[sl][blk][0][2], kb[sl][blk][0][3],
+                             kb[sl][blk][1][0], kb[sl][blk][1][1], kb[sl][blk][1][2], kb[sl][blk][1][3]};
+      dsa::f32x4 d[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+        d[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[mt], bf, zero, 0, 0, 0, 127, 0, 127);
+      const dsa::f32x4 du = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ua, bf, zero, 0, 0, 0, uscale, 0, 127);
+      if (g == blk) lin = (du[0] + du[1]) + (du[2] + du[3]);  // u.k of key 16 blk + c
+      float acc = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = fmaf(wh[mt][i], fabsf(d[mt][i]), acc);
+      ap[blk] = acc;
+    }
+    // reduce-scatter over the 4 lane groups: lane l ends with key kt0 + l
+    float r02, r13;
+    {
+      const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ap[0]), __float_as_uint(ap[2]), false, false);
+      r02 = __uint_as_float(s0[0]) + __uint_as_float(s0[1]);
+      const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ap[1]), __float_as_uint(ap[3]), false, false);
+      r13 = __uint_as_float(s1[0]) + __uint_as_float(s1[1]);
+    }
+    const auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(r02), __float_as_uint(r13), false, false);
+    float sum = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
+    sum += lin;
+    const int key = k0 + tile * kKeyTile + lane;
+    sum = key < L ? sum * ks[sl] : -__builtin_inff();
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sum), ost, (tile * kKeyTile + lane) * 4, 0, 0);
+    if (want_gmax) {
+      float m = sum;  // max over each 16-lane row, as in the kernel above
+      asm volatile(
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf"
+          : "+v"(m));
+      const int goff = c == 0 ? (tile * 4 + g) * 4 : 0x40000000;  // one lane per group; others dropped
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), gst, goff, 0, 0);
+    }
+  };
+
+  issue(0, dsa::IntC<0>{});
+  for (int it = 0; it < ntiles; it += kDecRing) {
+    issue(it + 1, dsa::IntC<1>{});
+    compute(it, dsa::IntC<0>{});
+    if (it + 1 >= ntiles) break;
+    issue(it + 2, dsa::IntC<0>{});
+    compute(it + 1, dsa::IntC<1>{});
+  }
+}
+
 }  // namespace
 
 namespace dsa {
@@ -487,6 +710,26 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
   p.S2 = S2;
   p.sparse_mode = sparse_mode;
   p.ntb = (S1 + kTokPerBlock - 1) / kTokPerBlock;
+  if (S1 <= kDecMaxTok) {
+    // decode form: one wave per (batch row, token, key chunk); chunks shrink to
+    // 256 keys until the launch has 2048 waves (8 per CU)
+    int dchunk = kDecMaxChunk;
+    while (dchunk > 4 * kKeyTile && (int64_t)B * S1 * ((S2 + dchunk - 1) / dchunk) < 2048) dchunk >>= 1;
+    p.chunk = dchunk;
+    p.nkc = (S2 + dchunk - 1) / dchunk;
+    p.ntb = 1;
+    const int64_t units = (int64_t)B * S1 * p.nkc;
+    const int64_t nwg = (units + kDecWaves - 1) / kDecWaves;
+    if (nwg <= 0) return kOk;
+    if (nwg > 0x7fffffff) return set_error(kUnsupported, "indexer: grid too large");
+    const bool paged = block_table != nullptr, scaled = key_scale != nullptr;
+    const dim3 grid((unsigned)nwg), blk(kDecWaves * 64);
+    if (paged && scaled) hipLaunchKernelGGL((indexer_decode_kernel<true, true>), grid, blk, 0, stream, p);
+    else if (paged) hipLaunchKernelGGL((indexer_decode_kernel<true, false>), grid, blk, 0, stream, p);
+    else if (scaled) hipLaunchKernelGGL((indexer_decode_kernel<false, true>), grid, blk, 0, stream, p);
+    else hipLaunchKernelGGL((indexer_decode_kernel<false, false>), grid, blk, 0, stream, p);
+    return check_launch("dsa_indexer_logits_fp8(decode)");
+  }
   // Shrink the key chunk (a multiple of the LDS tile) until the launch has one
   // workgroup per CU.  A workgroup's fixed cost (A operands, ring fill, the
   // group-maxima flush) is worth amortising over a longer chunk: with 32 query
