@@ -40,8 +40,8 @@ namespace {
 
 constexpr int kKT = 32;          // keys per step
 constexpr int kDV = 512;         // value dim
-constexpr int kWaves = 8;
-constexpr int kHeadsPerGroup = 16 * kWaves;
+constexpr int kWaves = 8;                        // waves of the 128-head workgroup
+constexpr int kHeadsPerGroup = 16 * kWaves;      // heads per head group (grid and workspace sizing)
 constexpr int kStagesWide = 4;  // ring stages when one workgroup fills a CU
 constexpr int kStagesPair = 2;  // ring stages when two workgroups share a CU
 constexpr int kMaxKeysPerSplit = 2048;
@@ -92,18 +92,27 @@ using dsa::xor32_sum;
 // Source of the gathers for invalid keys: always in bounds, always zero.
 __device__ __align__(16) uint16_t g_zero_row[576];
 
-template <int DQK, int kStages>
-__global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
-  constexpr int NT = kWaves * 64;
+// WAVES = 8: 128 heads per workgroup, one workgroup per CU.  WAVES = 4 (H <= 64,
+// e.g. DeepSeek-V4's 64 heads): 64 heads per workgroup and a 2-stage ring, so two
+// workgroups share a CU (2 waves per SIMD, <= 80 KB of LDS each) and one's
+// prologue / epilogue runs beside the other's steps instead of leaving half the
+// waves of a 128-head workgroup without heads.
+template <int DQK, int kStages, int WAVES>
+__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaParams p) {
+  constexpr int NT = WAVES * 64;
+  constexpr int HPG = 16 * WAVES;  // heads per workgroup
   constexpr int KSTEPS = DQK / 32;          // MFMA k-steps of the score product
   constexpr int NCH = DQK / 8;              // 16-byte chunks per KV row
   constexpr int STAGE = kKT * DQK * 2;      // bytes per ring stage
-  // wave w's i-th load fills block (kg = w % 4, cg = 2i + w / 4): waves 0-3 own
-  // the even chunk groups, waves 4-7 the odd ones
+  // wave w's i-th load fills block (kg = w % 4, cg = CGS i + w / 4): with 8 waves,
+  // waves 0-3 own the even chunk groups and waves 4-7 the odd ones; with 4 waves
+  // each wave loads every chunk group of its 8 keys
   static_assert(NCH % 8 == 0, "whole chunk groups");
+  static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
+  constexpr int CGS = WAVES / 4;                  // chunk-group stride of a wave's loads
   constexpr int NCG = NCH / 8;                    // chunk groups: 9 (576) or 8 (512)
-  constexpr int LOADS_HI = (NCG + 1) / 2;         // loads per step of waves 0-3
-  constexpr int LOADS_LO = NCG / 2;               // loads per step of waves 4-7
+  constexpr int LOADS_HI = (NCG + CGS - 1) / CGS; // loads per step of waves 0-3
+  constexpr int LOADS_LO = NCG / CGS;             // loads per step of waves 4-7
   static_assert(2 * LOADS_HI < 64, "vmcnt range");
 
   extern __shared__ __align__(16) unsigned char smem[];
@@ -129,9 +138,9 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
-  const int head = hg * kHeadsPerGroup + wave * 16 + c;
+  const int head = hg * HPG + wave * 16 + c;
   const bool head_ok = head < p.H;
-  const bool wave_active = hg * kHeadsPerGroup + wave * 16 < p.H;
+  const bool wave_active = hg * HPG + wave * 16 < p.H;
 
   const int kbeg = split * p.keys_per_split;
   const int nkeys = max(0, min(p.keys_per_split, p.topk - kbeg));
@@ -200,7 +209,7 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
   __syncthreads();  // rows[] ready
 
   // ---- gather of step `step` into ring stage step % kStages.  Wave w fills the
-  // blocks (kg = w % 4, cg = 2i + w / 4), i = 0, 1, ...; lane l loads in-block
+  // blocks (kg = w % 4, cg = CGS i + w / 4), i = 0, 1, ...; lane l loads in-block
   // key l / 8 and chunk (l % 8) ^ (l / 8) ^ (kg & 1), so it lands in slot l.
   const int gkg = wave & 3;
   const int gkey = 8 * gkg + (lane >> 3);
@@ -217,8 +226,8 @@ __global__ __launch_bounds__(kWaves * 64) void sparse_mla_kernel(MlaParams p) {
 #pragma unroll
     for (int i = 0; i < LOADS_HI; ++i) {
       if (i < LOADS_LO || many)
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + 8 * 16 * i),
-                                         (DSA_LDS void*)(sb + (i * kWaves + wave) * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + 64 * CGS * i),
+                                         (DSA_LDS void*)(sb + (i * WAVES + wave) * 1024), 16, 0, 0);
     }
   };
 
@@ -497,15 +506,15 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const uint16_t* __rest
   if (d8 == 0 && lse) lse[rh] = den > 0.f ? mx + __logf(den) : -__builtin_inff();
 }
 
-template <int DQK, int STAGES>
+template <int DQK, int STAGES, int WAVES>
 int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   const size_t smem = (size_t)STAGES * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split;
-  auto fn = sparse_mla_kernel<DQK, STAGES>;
+  auto fn = sparse_mla_kernel<DQK, STAGES, WAVES>;
   hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess)
     return dsa::set_error(dsa::kHipError, "sparse_mla: cannot reserve %zu bytes of LDS: %s", smem,
                           hipGetErrorString(e));
-  hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3(kWaves * 64), smem, stream, p);
+  hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3(WAVES * 64), smem, stream, p);
   return dsa::check_launch("dsa_sparse_mla_fwd");
 }
 
@@ -515,9 +524,10 @@ int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
 // dominated by gather latency and keep one workgroup per CU with a 4-stage ring.
 template <int DQK>
 int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
+  if (p.H <= 64) return launch_mla_stages<DQK, kStagesPair, 4>(p, nblocks, stream);
   if (nblocks >= 1024 && p.keys_per_split > 512)
-    return launch_mla_stages<DQK, kStagesPair>(p, nblocks, stream);
-  return launch_mla_stages<DQK, kStagesWide>(p, nblocks, stream);
+    return launch_mla_stages<DQK, kStagesPair, kWaves>(p, nblocks, stream);
+  return launch_mla_stages<DQK, kStagesWide, kWaves>(p, nblocks, stream);
 }
 
 int choose_splits(int64_t tokens, int nhg, int topk) {
