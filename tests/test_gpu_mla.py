@@ -77,6 +77,15 @@ def test_head_count_not_multiple_of_16(gpu):
     _check(inp, gpu)
 
 
+@pytest.mark.parametrize("H,topk,splits", [(64, 2048, 1), (64, 1024, 2), (96, 256, 1), (48, 512, 4)])
+def test_workgroup_forms(gpu, H, topk, splits):
+    # <= 64 heads: 4-wave workgroups (two per CU) unless their LDS does not fit
+    # (d_qk 576 with 2048-key lists: the 128-head form with idle waves); 65-127
+    # heads: the 128-head form with some waves idle; with and without splits
+    inp = inputs.mla_prefill(B=1, S=6, Skv=4096, H=H, topk=topk, seed=18 + H + topk)
+    _check(inp, gpu, is_causal=False, num_splits=splits)
+
+
 def test_reference_factory_fp16_sentinel_convention(gpu):
     # sparse_attention_fwd pads indices with the sentinel Skv (example_sparse_flash_attn.py:303)
     inp = inputs.mla_prefill(B=1, S=32, Skv=1024, H=128, topk=256, seed=17, q_start=900)

@@ -524,7 +524,11 @@ int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
 // dominated by gather latency and keep one workgroup per CU with a 4-stage ring.
 template <int DQK>
 int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
-  if (p.H <= 64) return launch_mla_stages<DQK, kStagesPair, 4>(p, nblocks, stream);
+  // 64 or fewer heads: 4-wave workgroups, when two of them fit in a CU's 160 KB
+  // of LDS (not at d_qk = 576 with 2048-key lists: the 128-head form then).
+  // Two 64-head workgroups per CU measured slower than one of 128 heads for H = 128.
+  const size_t lds4 = (size_t)kStagesPair * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split + 64;
+  if (p.H <= 64 && 2 * lds4 <= 160 * 1024) return launch_mla_stages<DQK, kStagesPair, 4>(p, nblocks, stream);
   if (nblocks >= 1024 && p.keys_per_split > 512)
     return launch_mla_stages<DQK, kStagesPair, kWaves>(p, nblocks, stream);
   return launch_mla_stages<DQK, kStagesWide, kWaves>(p, nblocks, stream);
