@@ -16,10 +16,11 @@
 // the gather) and one slice ("split") of the token's index list.  The indexed
 // KV rows (1152 bytes each) are gathered 32 at a time straight into an LDS ring
 // with global_load_lds (no staging registers): 4 stages (three steps in flight
-// while one is computed) when one workgroup fills a CU, or 2 stages when two
-// workgroups share a CU so that one's prologue and epilogue overlap the other's
-// steps (prefill).  A stage is 36 blocks of 1 KB; block (key group kg,
-// chunk group cg) at (cg * 4 + kg) * 1024 holds keys 8kg .. 8kg+7 x 16-byte chunks
+// while one is computed) for short lists, 2 stages for long ones (measured
+// faster there) and for the 4-wave workgroups, two of which share a CU so that
+// one's prologue and epilogue overlap the other's steps.  A stage is 36 blocks
+// of 1 KB; block (key group kg, chunk group cg) at (cg * 4 + kg) * 1024 holds
+// keys 8kg .. 8kg+7 x 16-byte chunks
 // 8cg .. 8cg+7, key-major, with chunk c of key k (in-block indices) stored at
 // slot k * 8 + (c ^ k ^ (kg & 1)).  One global_load_lds then fetches whole
 // 128-byte lines (8 chunks of one key per 8 lanes), and the XOR swizzle keeps
@@ -518,10 +519,12 @@ int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   return dsa::check_launch("dsa_sparse_mla_fwd");
 }
 
-// Two workgroups per CU (2-stage ring, <= 80 KB of LDS each) overlap one's
-// prologue and epilogue with the other's steps: used when there are many
-// workgroups with long index lists (prefill).  Short lists (decode splits) are
-// dominated by gather latency and keep one workgroup per CU with a 4-stage ring.
+// Ring depth and workgroup form.  An 8-wave workgroup (256 VGPRs per wave) fills
+// a CU's register file, so it runs alone on its CU: long index lists (prefill)
+// use a 2-stage ring (measured faster than 4 there), short ones (decode splits,
+// dominated by gather latency) a 4-stage ring.  4-wave workgroups pair up on a CU
+// with 2-stage rings (<= 80 KB of LDS each) and overlap one's prologue and
+// epilogue with the other's steps.
 template <int DQK>
 int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   // 64 or fewer heads: 4-wave workgroups, when two of them fit in a CU's 160 KB
