@@ -15,7 +15,7 @@
 // up to 128 heads (one 16-head MFMA tile per wave; waves past H only help with
 // the gather) and one slice ("split") of the token's index list.  The indexed
 // KV rows (1152 bytes each) are gathered 32 at a time straight into an LDS ring
-// with global_load_lds (no staging registers): 4 stages (three steps in flight
+// with global_load_lds (no staging registers): 3 stages (two steps in flight
 // while one is computed) for short lists, 2 stages for long ones (measured
 // faster there) and for the 4-wave workgroups, two of which share a CU so that
 // one's prologue and epilogue overlap the other's steps.  A stage is 36 blocks
@@ -43,8 +43,8 @@ constexpr int kKT = 32;          // keys per step
 constexpr int kDV = 512;         // value dim
 constexpr int kWaves = 8;                        // waves of the 128-head workgroup
 constexpr int kHeadsPerGroup = 16 * kWaves;      // heads per head group (grid and workspace sizing)
-constexpr int kStagesWide = 4;  // ring stages when one workgroup fills a CU
-constexpr int kStagesPair = 2;  // ring stages when two workgroups share a CU
+constexpr int kStagesWide = 3;  // ring stages for short lists (3 measured 2 % faster than 4 at decode)
+constexpr int kStagesPair = 2;  // ring stages for long lists and for 4-wave workgroups
 constexpr int kMaxKeysPerSplit = 2048;
 constexpr float kSlack = 8.f;    // log2 headroom of the reference maximum
 
@@ -521,8 +521,8 @@ int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
 
 // Ring depth and workgroup form.  An 8-wave workgroup (256 VGPRs per wave) fills
 // a CU's register file, so it runs alone on its CU: long index lists (prefill)
-// use a 2-stage ring (measured faster than 4 there), short ones (decode splits,
-// dominated by gather latency) a 4-stage ring.  4-wave workgroups pair up on a CU
+// use a 2-stage ring (measured faster than 3 or 4 there), short ones (decode
+// splits, dominated by gather latency) a 3-stage ring (2 % faster than 4).  4-wave workgroups pair up on a CU
 // with 2-stage rings (<= 80 KB of LDS each) and overlap one's prologue and
 // epilogue with the other's steps.
 template <int DQK>
