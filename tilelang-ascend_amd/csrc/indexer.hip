@@ -48,7 +48,8 @@ constexpr int kKeyLoaders = kTileBytes / 1024;   // waves 0..7 load 1 KB of keys
 constexpr int kScaleLoader = kKeyLoaders;        // wave 8 loads the tile's key scales
 constexpr int kSplits = 4;                       // fp8 pieces of u
 constexpr int kE4m3Max = 448;
-constexpr int kMaxChunk = 4096;                  // keys per workgroup at most
+constexpr int kMaxChunk = 16384;                 // keys per workgroup at most
+constexpr int kBaseChunk = 4096;                 // largest chunk when the key groups do not split evenly over the XCDs
 
 struct IndexerParams {
   const uint8_t* q;        // [B, S1, 64, 128] fp8
@@ -735,7 +736,18 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
   // group-maxima flush) is worth amortising over a longer chunk: with 32 query
   // rows x 128K keys, 256 workgroups of 1024 keys take 39 us where 1024 of 256
   // keys took 70.
-  int chunk = kMaxChunk;
+  // The key groups (batch row, chunk) are dealt to the 8 XCDs whole, so a chunk
+  // longer than 4096 keys is taken only when the groups split evenly over them
+  // (16384-key chunks at 128K keys: 3.52 ms against 3.69, the query block being
+  // read by 8 workgroups instead of 32; at 32K they would leave 6 XCDs idle).
+  int chunk = kBaseChunk;
+  for (int c = kMaxChunk; c > kBaseChunk; c >>= 1) {
+    const int64_t g = (int64_t)B * ((S2 + c - 1) / c);
+    if (g % kNumXcd == 0 && g * p.ntb >= 256) {
+      chunk = c;
+      break;
+    }
+  }
   while (chunk > kKeyTile && (int64_t)B * p.ntb * ((S2 + chunk - 1) / chunk) < 256) chunk >>= 1;
   p.chunk = chunk;
   p.nkc = (S2 + chunk - 1) / chunk;
