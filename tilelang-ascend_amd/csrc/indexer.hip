@@ -49,7 +49,6 @@ constexpr int kScaleLoader = kKeyLoaders;        // wave 8 loads the tile's key 
 constexpr int kSplits = 4;                       // fp8 pieces of u
 constexpr int kE4m3Max = 448;
 constexpr int kMaxChunk = 16384;                 // keys per workgroup at most
-constexpr int kBaseChunk = 4096;                 // largest chunk when the key groups do not split evenly over the XCDs
 
 struct IndexerParams {
   const uint8_t* q;        // [B, S1, 64, 128] fp8
@@ -70,6 +69,7 @@ struct IndexerParams {
   int64_t ld_g;
   int B, S1, S2, sparse_mode;
   int chunk, ntb, nkc;
+  int64_t per_xcd;        // work items (key group, token block) per XCD
 };
 
 __device__ __forceinline__ int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
@@ -137,13 +137,15 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   __shared__ int uexp[kWaves];
   __shared__ __align__(16) float lin[2][kWaves][kKeyTile];  // u.k per token and key, two tiles
 
-  // XCD-aware mapping: key groups (b, chunk) are dealt to XCDs, all token blocks
-  // of one key group run on the same XCD.
+  // XCD-aware mapping: the work items (key group (b, chunk), token block), key
+  // group major, are cut into 8 equal contiguous ranges, one per XCD (workgroup
+  // ids are dealt to the XCDs round-robin), so the XCDs get equal work and the
+  // workgroups sharing a key chunk run on one XCD, its keys in that XCD's L2.
   const int bid = blockIdx.x;
   const int xcd = bid % dsa::kNumXcd, r = bid / dsa::kNumXcd;
-  const int kg = xcd + dsa::kNumXcd * (r / p.ntb);
-  const int tb = r % p.ntb;
-  if (kg >= p.B * p.nkc) return;
+  const int64_t witem = (int64_t)xcd * p.per_xcd + r;
+  if (r >= p.per_xcd || witem >= (int64_t)p.B * p.nkc * p.ntb) return;
+  const int kg = (int)(witem / p.ntb), tb = (int)(witem % p.ntb);
   const int b = kg / p.nkc, kc = kg % p.nkc;
 
   // Rows of batch b: varlen (prefix sums) or padded [B, S1] / [B, S2].
@@ -719,6 +721,7 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
     p.chunk = dchunk;
     p.nkc = (S2 + dchunk - 1) / dchunk;
     p.ntb = 1;
+    p.per_xcd = 0;
     const int64_t units = (int64_t)B * S1 * p.nkc;
     const int64_t nwg = (units + kDecWaves - 1) / kDecWaves;
     if (nwg <= 0) return kOk;
@@ -736,23 +739,15 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
   // group-maxima flush) is worth amortising over a longer chunk: with 32 query
   // rows x 128K keys, 256 workgroups of 1024 keys take 39 us where 1024 of 256
   // keys took 70.
-  // The key groups (batch row, chunk) are dealt to the 8 XCDs whole, so a chunk
-  // longer than 4096 keys is taken only when the groups split evenly over them
-  // (16384-key chunks at 128K keys: 3.52 ms against 3.69, the query block being
-  // read by 8 workgroups instead of 32; at 32K they would leave 6 XCDs idle).
-  int chunk = kBaseChunk;
-  for (int c = kMaxChunk; c > kBaseChunk; c >>= 1) {
-    const int64_t g = (int64_t)B * ((S2 + c - 1) / c);
-    if (g % kNumXcd == 0 && g * p.ntb >= 256) {
-      chunk = c;
-      break;
-    }
-  }
+  // Long chunks also cut the re-reads of the query block (read once per chunk):
+  // 16384-key chunks at 128K keys take 3.44 ms against 3.61 with 4096.
+  int chunk = kMaxChunk;
   while (chunk > kKeyTile && (int64_t)B * p.ntb * ((S2 + chunk - 1) / chunk) < 256) chunk >>= 1;
   p.chunk = chunk;
   p.nkc = (S2 + chunk - 1) / chunk;
-  const int64_t groups = (int64_t)B * p.nkc;
-  const int64_t nblocks = ((groups + kNumXcd - 1) / kNumXcd) * kNumXcd * p.ntb;
+  const int64_t work = (int64_t)B * p.nkc * p.ntb;
+  p.per_xcd = (work + kNumXcd - 1) / kNumXcd;
+  const int64_t nblocks = p.per_xcd * kNumXcd;
   if (nblocks <= 0) return kOk;
   if (nblocks > 0x7fffffff) return set_error(kUnsupported, "indexer: grid too large");
   if (block_table != nullptr)
