@@ -384,3 +384,49 @@ def test_decode_form_shared_pool(gpu):
     # one row against the oracle
     _, rs, _ = ref_indexer(q[:1], kc[:1], w[:1], key_scale=kscale[:1], sparse_count=K, sparse_mode=0)
     _logit_close(lp[0, 0], rs[0, 0, 0])
+
+
+def test_paged_long_chunks_match_contiguous(gpu):
+    # enough query rows for 16384-key chunks (the paged form keeps a chunk's pool
+    # rows in LDS): paged and contiguous layouts give bit-identical logits, and
+    # sampled rows match the oracle
+    from dsa import _lib
+    B, S1, S2, bs = 4, 512, 20000, 64
+    inp = inputs.indexer_fp8(B=B, S1=S1, S2=S2, seed=404)
+    nb = (S2 + bs - 1) // bs
+    g = torch.Generator().manual_seed(404)
+    perm = torch.randperm(B * nb, generator=g)
+    pool = torch.zeros((B * nb, bs, 128), dtype=torch.uint8)
+    pscale = torch.zeros((B * nb, bs))
+    bt = perm.view(B, nb).int().contiguous()
+    kf = inp["k"].view(torch.uint8).view(B, S2, 128)
+    for b in range(B):
+        for j in range(nb):
+            lo, hi = j * bs, min(S2, (j + 1) * bs)
+            pool[bt[b, j], :hi - lo] = kf[b, lo:hi]
+            pscale[bt[b, j], :hi - lo] = inp["key_scale"][b, lo:hi]
+    d = {k: v.to(gpu) for k, v in inp.items()}
+    pool_d, ps_d, bt_d = pool.to(gpu), pscale.to(gpu), bt.to(gpu)
+    lc = torch.empty((B * S1, S2), device=gpu)
+    lp = torch.empty((B * S1, S2), device=gpu)
+    rl = torch.empty((B * S1,), dtype=torch.int32, device=gpu)
+    rl2 = torch.empty((B * S1,), dtype=torch.int32, device=gpu)
+    st = torch.cuda.current_stream().cuda_stream
+    print("indexer paged long chunks", flush=True)
+    L = _lib.lib()
+    _lib.check(L.dsa_indexer_logits_fp8(d["q"].data_ptr(), d["k"].data_ptr(), d["key_scale"].data_ptr(), d["w"].data_ptr(),
+                                        None, None, B, S1, S2, 64, 128, 3, lc.data_ptr(), S2, rl.data_ptr(), st), "contiguous")
+    _lib.check(L.dsa_indexer_logits_fp8_varlen(d["q"].data_ptr(), pool_d.data_ptr(), ps_d.data_ptr(), d["w"].data_ptr(),
+                                               None, 0, None, 0, bt_d.data_ptr(), bs, nb, B * nb * bs, B, S1, S2, 64, 128,
+                                               3, lp.data_ptr(), S2, rl2.data_ptr(), st), "paged")
+    torch.cuda.synchronize()
+    lc, lp, rl = lc.cpu(), lp.cpu(), rl.cpu()
+    assert torch.equal(rl, rl2.cpu())
+    vis = torch.arange(S2)[None, :] < rl[:, None].long()
+    assert torch.equal(lc[vis], lp[vis])
+    for b, t in ((0, 0), (1, 300), (3, S1 - 1)):
+        _, rs, _ = ref_indexer(inp["q"][b:b + 1, t:t + 1], inp["k"][b:b + 1, :S2 - S1 + t + 1], inp["w"][b:b + 1, t:t + 1],
+                               key_scale=inp["key_scale"][b:b + 1, :S2 - S1 + t + 1], sparse_count=64, sparse_mode=0)
+        n = S2 - S1 + t + 1
+        assert int(rl[b * S1 + t]) == n
+        _logit_close(lc[b * S1 + t, :n], rs[0, 0, 0, :n])
