@@ -168,3 +168,20 @@ def test_python_layer_rejects_bad_arguments():
     with pytest.raises(NotImplementedError, match="d = 512"):
         dsa.sparse_attn(torch.zeros(1, 2, 16, 256, dtype=bf), torch.zeros(1, 8, 256, dtype=bf),
                         torch.zeros(16), torch.zeros(1, 2, 4, dtype=torch.int32), 0.1)
+    q3 = torch.zeros(2, 128, 512, dtype=bf)
+    key = torch.zeros(4, 64, 1, 512, dtype=bf)
+    idx = torch.zeros(2, 1, 16, dtype=torch.int32)
+    one = torch.ones(1, dtype=torch.int32)
+    bt = torch.zeros(1, 4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="sparse_block_size"):
+        dsa.sparse_attn_tilelang(q3, key, key, idx, 0.5, 2, one, one, block_table=bt)
+    with pytest.raises(ValueError, match="sparse_mode"):
+        dsa.sparse_attn_tilelang(q3, key, key, idx, 0.5, 1, one, one, sparse_mode=1, block_table=bt)
+    with pytest.raises(ValueError, match="block_table"):
+        dsa.sparse_attn_tilelang(q3, key, key, idx, 0.5, 1, one, one)
+    with pytest.raises(ValueError, match="query_rope and key_rope"):
+        dsa.sparse_attn_tilelang(q3, key, key, idx, 0.5, 1, one, one, query_rope=torch.zeros(2, 128, 64, dtype=bf),
+                                 block_table=bt)
+    with pytest.raises(NotImplementedError, match="one batch"):
+        dsa.sparse_attn_tilelang(q3, key, key, idx, 0.5, 1, torch.ones(2, dtype=torch.int32),
+                                 torch.ones(2, dtype=torch.int32), block_table=torch.zeros(2, 4, dtype=torch.int32))
