@@ -308,6 +308,13 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
       want_gmax ? p.gmax + trow * p.ld_g + k0 / 16 : p.logits, (short)0,
       (want_gmax && tok_ok) ? ((kend - k0 + 15) / 16) * 4 : 0, 0x00020000);
 
+  // the u pieces' A operand, read once (loop invariant)
+  dsa::i32x8 ua;
+  {
+    dsa::i32x4 u0 = dsa::lds_read_b128<0>(ua_addr), u1 = dsa::lds_read_b128<16>(ua_addr);
+    lds_wait2<0>(u0, u1);
+    ua = dsa::i32x8{u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
+  }
   // The operand loads above complete before the ring starts, so the only vector
   // memory operations in flight inside the loop are the ring's and the stores.
   dsa::wait_vmcnt<0>();
@@ -339,8 +346,12 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
       float lk = lds_read_f32<lin_off>(lin_rd);
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lk));
       sum += lk;
-      const int key = k0 + tile * kKeyTile + lane;
-      sum = key < L ? sum * ksp : -__builtin_inff();
+      if (k0 + (tile + 1) * kKeyTile <= L) {  // the whole tile is visible (wave-uniform)
+        sum *= ksp;
+      } else {
+        const int key = k0 + tile * kKeyTile + lane;
+        sum = key < L ? sum * ksp : -__builtin_inff();
+      }
       voff = (tile * kKeyTile + lane) * 4;
     }
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sum), ost, voff, 0, 0);
@@ -426,11 +437,8 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
     });
     {
       // u.k of block ublk for the group's 4 tokens -> LDS (read in the next iteration).
-      dsa::i32x4 u0 = dsa::lds_read_b128<0>(ua_addr), u1 = dsa::lds_read_b128<16>(ua_addr);
       dsa::i32x4 k0v = dsa::lds_read_b128<so>(ub_rd0), k1v = dsa::lds_read_b128<so>(ub_rd1);
-      lds_wait2<0>(u0, u1);
       lds_wait2<0>(k0v, k1v);
-      const dsa::i32x8 ua = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
       const dsa::i32x8 ub = {k0v[0], k0v[1], k0v[2], k0v[3], k1v[0], k1v[1], k1v[2], k1v[3]};
       const dsa::f32x4 du = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ua, ub, zero, 0, 0, 0, uscale, 0, 127);
       const float lv = (du[0] + du[1]) + (du[2] + du[3]);
