@@ -329,8 +329,8 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   // Epilogue of a finished tile: reduce-scatter of the partial sums, plus u.k,
   // times the key scale, masked, stored.  tile < 0 issues a store that the
   // buffer range check drops, so every iteration has exactly one store.
-  auto finish = [&](const float (&ap)[4], float ksp, int tile, auto LB, auto SLOT) {
-    constexpr uint32_t lin_off = decltype(LB)::value * kLinBuf;
+  // lk: this lane's u.k of the tile (read from LDS by the caller, already waited for).
+  auto finish = [&](const float (&ap)[4], float ksp, float lk, int tile, auto SLOT) {
     constexpr int kSlot = decltype(SLOT)::value;  // tile % 4, or -1: the last tile (run-time slot)
     float r02, r13;
     {
@@ -343,8 +343,6 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
     float sum = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
     int voff = 0x40000000;  // beyond any descriptor range: dropped
     if (tile >= 0) {
-      float lk = lds_read_f32<lin_off>(lin_rd);
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lk));
       sum += lk;
       if (k0 + (tile + 1) * kKeyTile <= L) {  // the whole tile is visible (wave-uniform)
         sum *= ksp;
@@ -407,6 +405,9 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
 
     float ksc = 1.f;
     if (sbase != nullptr) ksc = lds_read_f32<ST * kKeyTile * 4>(sc_addr);
+    // u.k of the previous tile (written before the barrier); issued ahead of the
+    // B fragments so that their first wait covers it
+    float lkp = lds_read_f32<((ST + 1) & 1) * kLinBuf>(lin_rd);
     float a[4];
     // B fragments of block blk (16 keys x 128 B); the next block's read is in
     // flight while the current block's MFMAs run.
@@ -417,7 +418,10 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
       if constexpr (blk < 3) {
         nb0 = dsa::lds_read_b128<so + (blk + 1) * 2048>(rd0);
         nb1 = dsa::lds_read_b128<so + (blk + 1) * 2048>(rd1);
-        lds_wait2<2>(b0, b1);
+        if constexpr (blk == 0)
+          asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(b0), "+v"(b1), "+v"(lkp));
+        else
+          lds_wait2<2>(b0, b1);
       } else {
         lds_wait2<0>(b0, b1);
       }
@@ -426,7 +430,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)  // D[row = head 16mt + 4g + i][col = key 16blk + c]
         d[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[mt], bf, zero, 0, 0, 0, 127, 0, 127);
-      if constexpr (blk == 0) finish(ap, ksp, it - 1, dsa::IntC<(ST + 1) & 1>{}, dsa::IntC<(ST + 3) & 3>{});
+      if constexpr (blk == 0) finish(ap, ksp, lkp, it - 1, dsa::IntC<(ST + 3) & 3>{});
       float acc = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
@@ -459,8 +463,9 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   __builtin_amdgcn_s_setprio(0);
   {
     const int last = ntiles - 1;
-    if (last & 1) finish(ap, ksp, last, dsa::IntC<1>{}, dsa::IntC<-1>{});
-    else finish(ap, ksp, last, dsa::IntC<0>{}, dsa::IntC<-1>{});
+    float lk = (last & 1) ? lds_read_f32<kLinBuf>(lin_rd) : lds_read_f32<0>(lin_rd);
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lk));
+    finish(ap, ksp, lk, last, dsa::IntC<-1>{});
   }
   // No LDS DMA may still be in flight when the workgroup's LDS is released.
   if (loader) dsa::wait_vmcnt<0>();
