@@ -299,6 +299,9 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
           kfr[f % kPre] = lds_read_b128<(fn >> 2) * 4096 + (fn & 1) * 2048>((fn >> 1) & 1 ? kq1 : kq0);
         acc[f & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dsa::bf16x8, cur), qf[f >> 1],
                                                              acc[f & 1], 0, 0, 0);
+        // keep the pipeline as written: fragment f + kPre's read, then MFMA f
+        // (the compiler's own order measured ~2 % slower)
+        __builtin_amdgcn_sched_barrier(0);
       });
 
       // validity of the step's 32 keys as a wave-uniform bit mask
@@ -392,6 +395,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
         }
         const dsa::i32x4 av = {v0[0], v0[1], v1[0], v1[1]};
         o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dsa::bf16x8, av), pbf, o[dt], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       });
     }
   }
