@@ -1,7 +1,8 @@
 """GPU parity of the fp8 lightning indexer.
 
-Logits: within 1e-2 relative of the oracle, checked as
-|gpu - ref| <= 1e-2 * |ref| + 1e-2 * rms(ref row).  Indices: the top-k of the GPU's
+Logits: within 1e-2 relative of the oracle for every logit whose
+magnitude is at least 2 % of its row's RMS; smaller logits (cancellations of the
+signed head weights) within 2e-4 of the row RMS.  Indices: the top-k of the GPU's
 own logits is bit-exact with the oracle's stable top-k of the same logits; against
 the oracle's logits the reference's own acceptance rule applies
 (examples/deepseek_v4/lightning_indexer.py:1394-1503: differing indices must lie
@@ -18,13 +19,21 @@ pytestmark = pytest.mark.gpu
 
 
 def _logit_close(got, ref):
+    """1e-2 relative for every logit at or above a floor of 2 % of its row's RMS;
+    below the floor (near-cancellations of the signed head weights, where a
+    relative bound says nothing) the error must stay under 1e-2 of the floor."""
     fin = torch.isfinite(ref)
     assert torch.equal(fin, torch.isfinite(got)), "masked positions differ"
     rms = torch.sqrt(torch.mean(torch.where(fin, ref, 0) ** 2, dim=-1, keepdim=True))
+    floor = 2e-2 * rms
     err = (got - ref).abs()
-    tol = 1e-2 * ref.abs() + 1e-2 * rms
-    bad = (err > tol) & fin
-    assert not bad.any(), f"{int(bad.sum())} logits off, max err {float(err[fin].max())}"
+    big = (ref.abs() >= floor) & fin
+    rel = (err / ref.abs().clamp_min(1e-30))[big]
+    max_rel = float(rel.max()) if rel.numel() else 0.0
+    print(f"indexer logits: max relative error {max_rel:.3e} over {rel.numel()} entries above the floor", flush=True)
+    assert max_rel <= 1e-2, f"max relative error {max_rel}"
+    bad = (err > 1e-2 * floor) & fin & ~big
+    assert not bad.any(), f"{int(bad.sum())} logits below the floor off by more than 1e-2 of it"
 
 
 def _case(gpu, B, S1, S2, seed, K=2048, mode=3, act_q=None, act_k=None):

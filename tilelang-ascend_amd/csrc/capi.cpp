@@ -29,6 +29,21 @@ int check_launch(const char* what) {
   return kOk;
 }
 
+int reserve_lds(const void* fn, size_t bytes, std::atomic<int>* per_device, const char* what) {
+  int dev = -1;
+  const bool cached = hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices;
+  if (cached && per_device[dev].load(std::memory_order_relaxed) >= (int)bytes) return kOk;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess)
+    return set_error(kHipError, "%s: cannot reserve %zu bytes of LDS: %s", what, bytes, hipGetErrorString(e));
+  if (cached) {
+    int cur = per_device[dev].load(std::memory_order_relaxed);
+    while (cur < (int)bytes && !per_device[dev].compare_exchange_weak(cur, (int)bytes)) {
+    }
+  }
+  return kOk;
+}
+
 }  // namespace dsa
 
 extern "C" {

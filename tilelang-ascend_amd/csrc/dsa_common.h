@@ -5,6 +5,8 @@
 #include <stdint.h>
 #include <stddef.h>
 
+#include <atomic>
+
 namespace dsa {
 
 // Records a printf-style message as this thread's last error (read back through
@@ -14,6 +16,15 @@ int set_error(int code, const char* fmt, ...);
 // Checks the launch that was just made; on failure records `what` plus the HIP
 // error string and returns a non-zero code.
 int check_launch(const char* what);
+
+// Devices whose per-kernel LDS reservations are cached (more are served uncached).
+constexpr int kMaxDevices = 64;
+
+// Raises kernel `fn`'s dynamic LDS limit to at least `bytes` on the current
+// device.  `per_device` (one slot per device, zero-initialised, owned by the
+// kernel instance) remembers the largest reservation made, so the attribute call
+// runs once per kernel, device and size increase rather than on every launch.
+int reserve_lds(const void* fn, size_t bytes, std::atomic<int>* per_device, const char* what);
 
 enum Code : int {
   kOk = 0,

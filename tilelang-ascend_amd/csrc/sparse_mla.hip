@@ -515,10 +515,9 @@ template <int DQK, int STAGES, int WAVES>
 int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   const size_t smem = (size_t)STAGES * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split;
   auto fn = sparse_mla_kernel<DQK, STAGES, WAVES>;
-  hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-  if (e != hipSuccess)
-    return dsa::set_error(dsa::kHipError, "sparse_mla: cannot reserve %zu bytes of LDS: %s", smem,
-                          hipGetErrorString(e));
+  static std::atomic<int> lds_reserved[dsa::kMaxDevices];
+  const int rc = dsa::reserve_lds((const void*)fn, smem, lds_reserved, "sparse_mla");
+  if (rc != dsa::kOk) return rc;
   hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3(WAVES * 64), smem, stream, p);
   return dsa::check_launch("dsa_sparse_mla_fwd");
 }

@@ -885,7 +885,9 @@ int launch_rows(const TopkArgs& a, int64_t rows, hipStream_t stream) {
   constexpr int kCand = kCandCap > P2 + kBucketMax ? kCandCap : P2 + kBucketMax;
   const size_t smem = ((sizeof(Shared) + 15) & ~size_t(15)) + sizeof(uint64_t) * (size_t)(kSel + kCand);
   auto fn = topk_rows_kernel<ITEMS, EPT>;
-  (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  static std::atomic<int> lds_reserved[dsa::kMaxDevices];
+  const int rc = dsa::reserve_lds((const void*)fn, smem, lds_reserved, "dsa_topk_f32");
+  if (rc != dsa::kOk) return rc;
   hipLaunchKernelGGL(fn, dim3((unsigned)rows), dim3(kThreads), smem, stream, a);
   return dsa::check_launch("dsa_topk_f32");
 }

@@ -52,6 +52,14 @@ def _require_contiguous(name: str, t: torch.Tensor) -> None:
         raise ValueError(f"Expected {name} to be contiguous")
 
 
+def _host_lengths(t) -> torch.Tensor:
+    """Per-batch lengths / prefix sums as a host int64 vector: the grid sizes derive
+    from them, so the host needs their values (the reference reads them on the host
+    too, examples/deepseek_v4/lightning_indexer.py:1265-1279).  One device-to-host
+    copy when they live on the GPU, none when the caller passes them on the CPU."""
+    return torch.as_tensor(t).reshape(-1).to(device="cpu", dtype=torch.int64)
+
+
 def _int32_vec(name: str, t: Optional[torch.Tensor], n: int, device) -> Optional[torch.Tensor]:
     if t is None:
         return None
@@ -201,14 +209,15 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
         if actual_seq_lengths_query is None:
             raise AssertionError("TND layout requires actual_seq_lengths_query (prefix sums)")
         q_tot, N1, D = query.shape
-        cum_q = actual_seq_lengths_query.to(device=dev, dtype=torch.int32).contiguous()
-        B = cum_q.shape[0]
-        if B == 0 or int(cum_q[-1].item()) != q_tot:
+        cum_h = _host_lengths(actual_seq_lengths_query)
+        B = cum_h.shape[0]
+        if B == 0 or int(cum_h[-1]) != q_tot:
             raise ValueError(f"actual_seq_lengths_query must be prefix sums ending at T = {q_tot}")
-        q_lens = torch.diff(cum_q, prepend=torch.zeros(1, dtype=torch.int32, device=dev))
+        q_lens = torch.diff(cum_h, prepend=torch.zeros(1, dtype=torch.int64))
         if bool((q_lens < 0).any()):
             raise ValueError("actual_seq_lengths_query must be non-decreasing prefix sums")
-        S1 = int(q_lens.max().item())
+        S1 = int(q_lens.max())
+        cum_q = cum_h.to(device=dev, dtype=torch.int32)
         if tuple(weights.shape) != (q_tot, N1):
             raise ValueError(f"weights must be [T, N1] = {(q_tot, N1)}, got {tuple(weights.shape)}")
         seq_q, seq_q_cum = cum_q, 1
@@ -238,10 +247,11 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
             raise ValueError(f"block_table must be [B, max_blocks], got {tuple(block_table.shape)}")
         bt = block_table.to(device=dev, dtype=torch.int32).contiguous()
         max_blocks, pool_rows = bt.shape[1], nblk * block_size
-        seq_k, seq_k_cum = actual_seq_lengths_key.to(device=dev, dtype=torch.int32).contiguous(), 0
-        if seq_k.numel() != B:
-            raise ValueError(f"actual_seq_lengths_key must have B = {B} entries, got {seq_k.numel()}")
-        S2 = int(seq_k.max().item()) if B > 0 else 0
+        seq_h = _host_lengths(actual_seq_lengths_key)
+        if seq_h.numel() != B:
+            raise ValueError(f"actual_seq_lengths_key must have B = {B} entries, got {seq_h.numel()}")
+        S2 = int(seq_h.max()) if B > 0 else 0
+        seq_k, seq_k_cum = seq_h.to(device=dev, dtype=torch.int32), 0
         k_tokens = pool_rows
     elif is_tnd_key:
         if key.dim() != 3:
@@ -249,13 +259,14 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
         if actual_seq_lengths_key is None:
             raise AssertionError("TND layout requires actual_seq_lengths_key (prefix sums)")
         k_tot, N2, Dk = key.shape
-        seq_k, seq_k_cum = actual_seq_lengths_key.to(device=dev, dtype=torch.int32).contiguous(), 1
-        if seq_k.numel() != B or (B > 0 and int(seq_k[-1].item()) != k_tot):
+        seq_h = _host_lengths(actual_seq_lengths_key)
+        if seq_h.numel() != B or (B > 0 and int(seq_h[-1]) != k_tot):
             raise ValueError(f"actual_seq_lengths_key must be {B} prefix sums ending at T2 = {k_tot}")
-        k_lens = torch.diff(seq_k, prepend=torch.zeros(1, dtype=torch.int32, device=dev))
+        k_lens = torch.diff(seq_h, prepend=torch.zeros(1, dtype=torch.int64))
         if bool((k_lens < 0).any()):
             raise ValueError("actual_seq_lengths_key must be non-decreasing prefix sums")
-        S2 = int(k_lens.max().item()) if B > 0 else 0
+        S2 = int(k_lens.max()) if B > 0 else 0
+        seq_k, seq_k_cum = seq_h.to(device=dev, dtype=torch.int32), 1
         k_tokens = k_tot
     else:
         if key.dim() != 4:
@@ -715,7 +726,7 @@ def sparse_flash_mla(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[
     elif scenario == 2:
         N2 = cmp_kv.shape[2]
         cmp_idx, K = None, 0
-        n_cmp = int(seqused_kv.max().item()) // cmp_ratio
+        n_cmp = int(_host_lengths(seqused_kv).max()) // cmp_ratio
     else:
         cmp_idx, K, n_cmp = None, 0, 0
     if N1 != 64 or N2 != 1 or D != 512:
