@@ -198,6 +198,27 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices,
                        void* stream);
 
 /*
+ * dsa_sparse_mla_fwd without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, results and kernels as dsa_sparse_mla_fwd; the
+ * split partials go to a fixed array of DSA_SPARSE_MLA_SCRATCH_BYTES per GPU,
+ * resident from the library's first call on that GPU until the process ends.
+ * Calls whose partials need more (dsa_sparse_mla_workspace_bytes(...) above the
+ * limit) return DSA_E_WORKSPACE_TOO_SMALL.  Every call on one GPU shares that
+ * array, which keeps the last call's contents (each call writes every partial it
+ * reads, so nothing needs clearing): calls that overlap on one GPU (concurrent
+ * streams or threads) race and must be serialised by the caller.
+ */
+#define DSA_SPARSE_MLA_SCRATCH_BYTES ((size_t)64 << 20)
+int dsa_sparse_mla_fwd_noalloc(const void* q, const void* kv, const int32_t* indices,
+                               const int32_t* block_table, const int32_t* kv_len, const int32_t* q_start,
+                               const float* attn_sink, int64_t B, int64_t S, int32_t H, int32_t d_qk,
+                               int32_t d_v, int64_t skv, int32_t block_size, int32_t max_blocks,
+                               int32_t topk, float sm_scale, int32_t is_causal, int32_t num_splits,
+                               void* out, float* lse, void* stream);
+
+/*
  * Block-sparse indexer logits (the HISA second stage): replaces the call of
  * paged_block_sparse_mqa_attn_return_logits
  * (examples/HISA/paged_block_sparse_mqa_attn_expert.py:54-422; reference

@@ -34,6 +34,8 @@
 // reference maximum per head and rescales O only when a score exceeds it by
 // more than 2^8.  With more than one split the workgroups write normalised
 // partial outputs plus their LSE, and a combine kernel merges them.
+#include <mutex>
+
 #include "dsa_common.h"
 #include "mla_run.h"
 
@@ -646,9 +648,93 @@ int sparse_mla_run(const MlaRun& r, const char* what) {
 
 }  // namespace dsa
 
+// ---- the allocation-free entry point: split partials in a fixed device array ----
+namespace {
+
+constexpr size_t kScratchBytes = size_t(64) << 20;  // DSA_SPARSE_MLA_SCRATCH_BYTES
+
+// Split partials of dsa_sparse_mla_fwd_noalloc.  In host code this name is a
+// host-side stand-in, not a device address: only the pointer that
+// hipGetSymbolAddress returns for the current device may be passed to kernels or
+// memory calls.
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[dsa::kMaxDevices];  // device address of `scratch`, per device
+
+// Address of this device's copy of `scratch`, looked up on the first call on the
+// device (with that device current) and kept for the process's lifetime.
+int scratch_for_current_device(void** out, const char* what) {
+  int dev = -1;
+  const hipError_t ge = hipGetDevice(&dev);
+  if (ge != hipSuccess) return dsa::set_error(dsa::kHipError, "%s: hipGetDevice: %s", what, hipGetErrorString(ge));
+  if (dev < 0 || dev >= dsa::kMaxDevices)
+    return dsa::set_error(dsa::kUnsupported, "%s: device %d is beyond the %d supported", what, dev, dsa::kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return dsa::set_error(dsa::kHipError, "%s: hipGetSymbolAddress(scratch): %s", what, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return dsa::kOk;
+}
+
+}  // namespace
+
 extern "C" size_t dsa_sparse_mla_workspace_bytes(int64_t B, int64_t S, int32_t H, int32_t topk,
                                                  int32_t num_splits) {
   return dsa::sparse_mla_split_bytes(B * S, H, topk, num_splits);
+}
+
+extern "C" int dsa_sparse_mla_fwd_noalloc(const void* q, const void* kv, const int32_t* indices,
+                                          const int32_t* block_table, const int32_t* kv_len,
+                                          const int32_t* q_start, const float* attn_sink, int64_t B,
+                                          int64_t S, int32_t H, int32_t d_qk, int32_t d_v, int64_t skv,
+                                          int32_t block_size, int32_t max_blocks, int32_t topk,
+                                          float sm_scale, int32_t is_causal, int32_t num_splits, void* out,
+                                          float* lse, void* stream) {
+  const char* what = "dsa_sparse_mla_fwd_noalloc";
+  if (B < 0 || S < 0 || H <= 0 || topk < 0) return dsa::set_error(dsa::kInvalidArgument, "%s: bad sizes", what);
+  const size_t need = dsa::sparse_mla_split_bytes(B * S, H, topk, num_splits);
+  if (need > kScratchBytes)
+    return dsa::set_error(dsa::kWorkspaceTooSmall,
+                          "%s: the split partials need %zu bytes, above the fixed %zu-byte scratch; "
+                          "use fewer tokens or splits per call, or dsa_sparse_mla_fwd with a workspace",
+                          what, need, kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_for_current_device(&ws, what);
+    if (rc != dsa::kOk) return rc;
+  }
+  dsa::MlaRun r{};
+  r.q = q;
+  r.kv = kv;
+  r.indices = indices;
+  r.block_table = block_table;
+  r.kv_len = kv_len;
+  r.q_start = q_start;
+  r.attn_sink = attn_sink;
+  r.B = B;
+  r.S = S;
+  r.H = H;
+  r.d_qk = d_qk;
+  r.d_v = d_v;
+  r.skv = skv;
+  r.block_size = block_size;
+  r.max_blocks = max_blocks;
+  r.topk = topk;
+  r.sm_scale = sm_scale;
+  r.is_causal = is_causal;
+  r.num_splits = num_splits;
+  r.out = out;
+  r.lse = lse;
+  r.workspace = ws;
+  r.workspace_bytes = need > 0 ? kScratchBytes : 0;
+  r.stream = stream;
+  return dsa::sparse_mla_run(r, what);
 }
 
 extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices,

@@ -40,6 +40,9 @@ SIGNATURES = {
     "dsa_sparse_mla_fwd": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32,
                                    c_i32, c_i32, c_i64, c_i32, c_i32, c_i32, c_f32, c_i32, c_i32,
                                    c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "dsa_sparse_mla_fwd_noalloc": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32,
+                                           c_i32, c_i32, c_i64, c_i32, c_i32, c_i32, c_f32, c_i32, c_i32,
+                                           c_vp, c_vp, c_vp]),
     "dsa_sparse_flash_mla_workspace_bytes": (c_sz, [c_i64, c_i32, c_i32, c_i32]),
     "dsa_sparse_flash_mla": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i32, c_vp,
                                      c_i32, c_vp, c_i64, c_i32, c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_f32,
