@@ -11,29 +11,26 @@
 // valid index yields out = 0, lse = -inf.  An optional per-head sink adds
 // exp(sink - m) to the denominator (sparse_flash_mla_golden.py:115-149).
 //
-// Work decomposition.  One workgroup (8 waves, two per SIMD) handles one token,
-// up to 128 heads (one 16-head MFMA tile per wave; waves past H only help with
-// the gather) and one slice ("split") of the token's index list.  The indexed
-// KV rows (1152 bytes each) are gathered 32 at a time straight into an LDS ring
-// with global_load_lds (no staging registers): 3 stages (two steps in flight
-// while one is computed) for short lists, 2 stages for long ones (measured
-// faster there) and for the 4-wave workgroups, two of which share a CU so that
-// one's prologue and epilogue overlap the other's steps.  A stage is 36 blocks
-// of 1 KB; block (key group kg, chunk group cg) at (cg * 4 + kg) * 1024 holds
-// keys 8kg .. 8kg+7 x 16-byte chunks
-// 8cg .. 8cg+7, key-major, with chunk c of key k (in-block indices) stored at
-// slot k * 8 + (c ^ k ^ (kg & 1)).  One global_load_lds then fetches whole
-// 128-byte lines (8 chunks of one key per 8 lanes), and the XOR swizzle keeps
-// both LDS read patterns below free of bank conflicts.  Per wave and step:
-//   S^T[32 keys x 16 heads] = K[32 x Dqk] . Q^T        (v_mfma_f32_16x16x32_bf16)
-//   O^T[512 x 16 heads]    += V^T[512 x 32] . P^T
-// Computing S^T leaves each lane holding exactly the 8 probabilities (one head,
-// 8 keys) that the PV instruction takes as its B operand, so P never leaves
-// registers.  The V^T operand is read from the same tile with the transposing
+// Work decomposition.  One workgroup handles one token, up to 128 heads (a
+// "head group") and one slice ("split") of the token's index list.  The indexed
+// KV rows (1152 bytes each) are gathered 32 at a time ("steps") straight into an
+// LDS ring with global_load_lds (no staging registers), and both products run on
+// MFMA with the single KV tile read from LDS by every head:
+//   S^T[32 keys x heads] = K[32 x Dqk] . Q^T
+//   O^T[512 x heads]    += V^T[512 x 32] . P^T
+// Computing S^T leaves each lane holding exactly the probabilities (one head, 8
+// keys) that the P.V instruction takes as its B operand, so P never leaves
+// registers, and the V^T operand is read from the same tile with the transposing
 // LDS load ds_read_b64_tr_b16, so V is never copied.  The softmax keeps a
 // reference maximum per head and rescales O only when a score exceeds it by
-// more than 2^8.  With more than one split the workgroups write normalised
-// partial outputs plus their LSE, and a combine kernel merges them.
+// more than 2^8.  With more than one split the workgroups write fp16 partial
+// outputs plus their LSE, and a combine kernel merges them.
+//
+// Two workgroup forms (launch_mla):
+//  * more than 64 heads: 4 waves of 32 heads, one wave per SIMD holding Q^T and
+//    O^T in registers, v_mfma_f32_32x32x16_bf16, a 4-stage ring (mla_w4_kernel);
+//  * 64 heads or fewer: 4 waves of 16 heads (v_mfma_f32_16x16x32_bf16), a
+//    2-stage ring, two workgroups per CU (sparse_mla_kernel).
 #include <mutex>
 
 #include "dsa_common.h"
@@ -43,10 +40,8 @@ namespace {
 
 constexpr int kKT = 32;          // keys per step
 constexpr int kDV = 512;         // value dim
-constexpr int kWaves = 8;                        // waves of the 128-head workgroup
-constexpr int kHeadsPerGroup = 16 * kWaves;      // heads per head group (grid and workspace sizing)
-constexpr int kStagesWide = 3;  // ring stages for short lists (3 measured 2 % faster than 4 at decode)
-constexpr int kStagesPair = 2;  // ring stages for long lists and for 4-wave workgroups
+constexpr int kHeadsPerGroup = 128;  // heads per head group (grid and workspace sizing)
+constexpr int kStagesPair = 2;       // ring stages of the paired 64-head workgroups
 constexpr int kMaxKeysPerSplit = 2048;
 constexpr float kSlack = 8.f;    // log2 headroom of the reference maximum
 
@@ -95,11 +90,104 @@ using dsa::xor32_sum;
 // Source of the gathers for invalid keys: always in bounds, always zero.
 __device__ __align__(16) uint16_t g_zero_row[576];
 
-// WAVES = 8: 128 heads per workgroup, one workgroup per CU.  WAVES = 4 (H <= 64,
-// e.g. DeepSeek-V4's 64 heads): 64 heads per workgroup and a 2-stage ring, so two
-// workgroups share a CU (2 waves per SIMD, <= 80 KB of LDS each) and one's
-// prologue / epilogue runs beside the other's steps instead of leaving half the
-// waves of a 128-head workgroup without heads.
+// Physical row of each index of this split (-1 = skip): rows[j] for key kbeg + j of
+// the token's list, after the validity rules (range, page, causal) or the
+// DeepSeek-V4 key-set generation.  All NT threads of the workgroup take part.
+// mid() runs once the list's index loads are issued and before any is used, so
+// loads it issues (the query operands) overlap the resolution.
+struct NoMid {
+  __device__ void operator()() const {}
+};
+template <int NT, typename Mid = NoMid>
+__device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, int b, int s, int kbeg, int nkeys,
+                                             int32_t* rows, int tid, Mid mid = Mid{}) {
+  if (p.v4_on) {
+    mid();
+    __shared__ int v4_sh[2];  // batch of this row, first -1 of its compressed list
+    if (tid == 0) {
+      v4_sh[0] = dsa::v4_batch(p.v4, token);
+      v4_sh[1] = p.v4.K;
+    }
+    __syncthreads();
+    const int vb = v4_sh[0];
+    if (vb >= 0 && p.v4.scenario == 3) {
+      const int32_t* ci = p.v4.cmp_idx + token * p.v4.K;
+      for (int j = tid; j < p.v4.K; j += NT)
+        if (ci[j] == -1) atomicMin(&v4_sh[1], j);
+      __syncthreads();
+    }
+    const int stop = v4_sh[1];
+    for (int j = tid; j < nkeys; j += NT) rows[j] = vb >= 0 ? dsa::v4_row(p.v4, token, vb, kbeg + j, stop) : -1;
+  } else {
+    // every index load of the thread is issued before any is used, then every
+    // page-table load: two memory round trips for the whole list instead of one
+    // or two per 2048 / NT keys
+    constexpr int R = kMaxKeysPerSplit / NT;  // list entries per thread
+    const int kvl = p.kv_len ? p.kv_len[b] : (int)(p.skv < 0x7fffffff ? p.skv : 0x7fffffff);
+    const int qs = p.q_start ? p.q_start[b] : kvl - p.S;
+    // loads at clamped positions, without a branch per load (an empty list
+    // reads nothing), then selects
+    const int32_t* ip = p.indices + token * p.topk;
+    int idx[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      idx[r] = p.topk > 0 ? __builtin_nontemporal_load(ip + min(kbeg + tid + r * NT, p.topk - 1)) : -1;
+#pragma unroll
+    for (int r = 0; r < R; ++r) idx[r] = tid + r * NT < nkeys ? idx[r] : -1;
+    mid();
+    if (p.direct) {
+      // resolved rows: bit 30 selects the second pool
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int j = tid + r * NT;
+        const int rr = idx[r] & ~dsa::kRowTag2;
+        const bool ok = idx[r] >= 0 && (int64_t)rr < ((idx[r] & dsa::kRowTag2) ? p.pool_rows2 : p.pool_rows);
+        if (j < nkeys) rows[j] = ok ? idx[r] : -1;
+      }
+      return;
+    }
+    bool ok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      ok[r] = idx[r] >= 0 && idx[r] < kvl && (int64_t)idx[r] < p.skv;
+      if (p.causal) ok[r] = ok[r] && idx[r] <= qs + s;
+    }
+    if (p.block_table) {
+      int page[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int blk = idx[r] / p.block_size;
+        page[r] = ok[r] && blk < p.max_blocks ? p.block_table[(int64_t)b * p.max_blocks + blk] : -1;
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int j = tid + r * NT;
+        const int64_t rr = (int64_t)page[r] * p.block_size + idx[r] % p.block_size;
+        if (j < nkeys) rows[j] = page[r] >= 0 && rr < p.pool_rows ? (int32_t)rr : -1;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int j = tid + r * NT;
+        if (j < nkeys) rows[j] = ok[r] ? (int32_t)((int64_t)b * p.skv + idx[r]) : -1;
+      }
+    }
+  }
+}
+
+// 16-head-per-wave form.  A ring stage is 36 (or 32) blocks of 1 KB; block (key
+// group kg, chunk group cg) at (cg * 4 + kg) * 1024 holds keys 8kg .. 8kg+7 x
+// 16-byte chunks 8cg .. 8cg+7, key-major, with chunk c of key k (in-block
+// indices) stored at slot k * 8 + (c ^ k ^ (kg & 1)).  One global_load_lds then
+// fetches whole 128-byte lines (8 chunks of one key per 8 lanes), and the XOR
+// swizzle keeps both LDS read patterns free of bank conflicts.
+//
+// 16 heads per wave, WAVES waves per workgroup.  The library runs it with
+// WAVES = 4 for H <= 64 (e.g. DeepSeek-V4's 64 heads): 64 heads per workgroup and
+// a 2-stage ring, so two workgroups share a CU (2 waves per SIMD, <= 80 KB of LDS
+// each) and one's prologue / epilogue runs beside the other's steps.  (WAVES = 8,
+// one 128-head workgroup per CU, measured slower than the 4-wave 128-head form
+// below and is not launched.)
 template <int DQK, int kStages, int WAVES>
 __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaParams p) {
   constexpr int NT = WAVES * 64;
@@ -163,51 +251,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
   }
 
   // ---- resolve this split's indices to physical rows (-1 = skip) ----
-  if (p.v4_on) {
-    __shared__ int v4_sh[2];  // batch of this row, first -1 of its compressed list
-    if (tid == 0) {
-      v4_sh[0] = dsa::v4_batch(p.v4, token);
-      v4_sh[1] = p.v4.K;
-    }
-    __syncthreads();
-    const int vb = v4_sh[0];
-    if (vb >= 0 && p.v4.scenario == 3) {
-      const int32_t* ci = p.v4.cmp_idx + token * p.v4.K;
-      for (int j = tid; j < p.v4.K; j += NT)
-        if (ci[j] == -1) atomicMin(&v4_sh[1], j);
-      __syncthreads();
-    }
-    const int stop = v4_sh[1];
-    for (int j = tid; j < nkeys; j += NT) rows[j] = vb >= 0 ? dsa::v4_row(p.v4, token, vb, kbeg + j, stop) : -1;
-  } else {
-    const int kvl = p.kv_len ? p.kv_len[b] : (int)(p.skv < 0x7fffffff ? p.skv : 0x7fffffff);
-    const int qs = p.q_start ? p.q_start[b] : kvl - p.S;
-    const int32_t* ip = p.indices + token * p.topk + kbeg;
-    for (int j = tid; j < nkeys; j += NT) {
-      const int idx = ip[j];
-      int32_t row = -1;
-      if (p.direct) {
-        // resolved rows: bit 30 selects the second pool
-        const int r = idx & ~dsa::kRowTag2;
-        if (idx >= 0 && (int64_t)r < ((idx & dsa::kRowTag2) ? p.pool_rows2 : p.pool_rows)) row = idx;
-        rows[j] = row;
-        continue;
-      }
-      bool ok = idx >= 0 && idx < kvl && (int64_t)idx < p.skv;
-      if (ok && p.causal) ok = idx <= qs + s;
-      if (ok) {
-        if (p.block_table) {
-          const int blk = idx / p.block_size;
-          const int page = blk < p.max_blocks ? p.block_table[(int64_t)b * p.max_blocks + blk] : -1;
-          const int64_t rr = (int64_t)page * p.block_size + idx % p.block_size;
-          if (page >= 0 && rr < p.pool_rows) row = (int32_t)rr;
-        } else {
-          row = (int32_t)((int64_t)b * p.skv + idx);
-        }
-      }
-      rows[j] = row;
-    }
-  }
+  resolve_rows<NT>(p, token, b, s, kbeg, nkeys, rows, tid);
   wait_vmcnt<0>();  // Q operands are in registers before any gather is queued
   __syncthreads();  // rows[] ready
 
@@ -448,6 +492,577 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
   }
 }
 
+// ---------------------------------------------------------------------------
+// 128-head form (H > 64): four waves, one per SIMD, 32 heads each, on
+// v_mfma_f32_32x32x16_bf16.  Per wave and 32-key step:
+//   S^T[32 keys x 32 heads]  = sum over 36 k-steps of K[32 x 16] . Q^T[16 x 32]
+//   O^T[512 x 32 heads]     += V^T[512 x 32] . P^T[32 x 32]   (16 d-tiles x 2 k-steps)
+// A 32-head wave reads each K / V fragment once for 32 heads, half the LDS bytes
+// per MFMA of the 16-head form, and one wave per SIMD owns the whole register
+// file: Q^T (144 VGPRs at d_qk 576) and O^T (256 accumulators) stay resident.
+// With no second wave on the SIMD to fill the softmax gap, the loop is software
+// pipelined: step j runs the score MFMAs of key step j, then the P.V MFMAs of
+// step j - 1 with the softmax of step j spread between them.  A 4-stage LDS ring (3 steps of
+// gathers in flight) keeps one step for P.V, one for the scores and two loading.
+//
+// Register layouts (lane l, hh = l / 32, l32 = l % 32):
+//   32x32 result (S^T and O^T tiles), element r: row 8 (r / 4) + 4 hh + r % 4, column l32
+//   A operand: row l32, k-elements 8 hh .. 8 hh + 7;  B operand: column l32, same k
+// so the lane holding head l32's scores of keys {8 (r / 4) + 4 hh + r % 4} passes
+// exactly those as P^T for the k-slots 8 hh .. 8 hh + 7 of two P.V k-steps, with
+// k-slot i of k-step kk standing for key 16 kk + 8 (i / 4) + 4 hh + i % 4; the
+// V^T operand is read for the same keys with two transposing reads (4 keys each).
+// ---------------------------------------------------------------------------
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kW4Stages = 4;  // ring stages of the 4-wave form
+constexpr int kW4KPre = 4;    // score A fragments in flight
+constexpr int kW4VPre = 4;    // P.V A fragments (two reads each) in flight
+
+// The MFMAs of this form are issued as inline asm so that the register file stays
+// partitioned as designed.  The 256 O^T accumulators are not C++ values at all:
+// d-tile DT lives in a[16 DT .. 16 DT + 15], named in the asm text, and every
+// asm statement of the kernel that issues an MFMA or touches the AGPRs lists all
+// 256 AGPRs as clobbered, so the compiler neither places a value of its own
+// there nor leaves them out of the kernel's register count.  (As C++ values the
+// accumulators were copied into VGPRs around every MFMA and Q^T spilled.)  The
+// score accumulators, Q^T and the working set are ordinary VGPR values.  The
+// compiler does not insert MFMA hazard wait states for inline asm; the kernel
+// places them itself (mfma_drain) where a VALU instruction or a store reads an
+// MFMA result soon after it was written.  Chained MFMAs on one accumulator
+// (exactly overlapping srcC / vdst) need none.
+#define DSA_A10(p) \
+  "a" #p "0", "a" #p "1", "a" #p "2", "a" #p "3", "a" #p "4", "a" #p "5", "a" #p "6", "a" #p "7", "a" #p "8", "a" #p "9"
+#define DSA_AGPRS                                                                                                  \
+  "a0", "a1", "a2", "a3", "a4", "a5", "a6", "a7", "a8", "a9", DSA_A10(1), DSA_A10(2), DSA_A10(3), DSA_A10(4),        \
+      DSA_A10(5), DSA_A10(6), DSA_A10(7), DSA_A10(8), DSA_A10(9), DSA_A10(10), DSA_A10(11), DSA_A10(12), DSA_A10(13), \
+      DSA_A10(14), DSA_A10(15), DSA_A10(16), DSA_A10(17), DSA_A10(18), DSA_A10(19), DSA_A10(20), DSA_A10(21),        \
+      DSA_A10(22), DSA_A10(23), DSA_A10(24), "a250", "a251", "a252", "a253", "a254", "a255"
+
+// S^T = K . Q^T (first k-step) and S^T += K . Q^T, in VGPRs
+__device__ __forceinline__ void mfma32_v0(f32x16& acc, dsa::i32x4 a, dsa::i32x4 b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b) : DSA_AGPRS);
+}
+__device__ __forceinline__ void mfma32_v(f32x16& acc, dsa::i32x4 a, dsa::i32x4 b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b) : DSA_AGPRS);
+}
+// O^T d-tile DT += V^T . P^T
+template <int DT>
+__device__ __forceinline__ void mfma32_o(dsa::i32x4 a, dsa::i32x4 b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 a[%2:%3], %0, %1, a[%2:%3]"
+               :
+               : "v"(a), "v"(b), "i"(16 * DT), "i"(16 * DT + 15)
+               : DSA_AGPRS);
+}
+// O^T = 0
+__device__ __forceinline__ void zero_o() {
+  asm volatile(
+      ".set .Ldsa_acc, 0\n"
+      ".rept 256\n"
+      "v_accvgpr_write_b32 a[.Ldsa_acc], 0\n"
+      ".set .Ldsa_acc, .Ldsa_acc + 1\n"
+      ".endr" ::
+          : DSA_AGPRS);
+}
+// O^T *= alpha, one register at a time through one VGPR (the rescale is rare)
+__device__ __forceinline__ void scale_o(float alpha) {
+  float t;
+  asm volatile(
+      ".set .Ldsa_acc, 0\n"
+      ".rept 256\n"
+      "v_accvgpr_read_b32 %0, a[.Ldsa_acc]\n"
+      "v_mul_f32 %0, %0, %1\n"
+      "v_accvgpr_write_b32 a[.Ldsa_acc], %0\n"
+      ".set .Ldsa_acc, .Ldsa_acc + 1\n"
+      ".endr"
+      : "=&v"(t)
+      : "v"(alpha)
+      : DSA_AGPRS);
+}
+// the 16 values of O^T d-tile DT
+template <int DT>
+__device__ __forceinline__ void read_o(float (&t)[16]) {
+  asm volatile(
+      ".set .Ldsa_acc, %16\n"
+      "v_accvgpr_read_b32 %0, a[.Ldsa_acc]\n"
+      "v_accvgpr_read_b32 %1, a[.Ldsa_acc + 1]\n"
+      "v_accvgpr_read_b32 %2, a[.Ldsa_acc + 2]\n"
+      "v_accvgpr_read_b32 %3, a[.Ldsa_acc + 3]\n"
+      "v_accvgpr_read_b32 %4, a[.Ldsa_acc + 4]\n"
+      "v_accvgpr_read_b32 %5, a[.Ldsa_acc + 5]\n"
+      "v_accvgpr_read_b32 %6, a[.Ldsa_acc + 6]\n"
+      "v_accvgpr_read_b32 %7, a[.Ldsa_acc + 7]\n"
+      "v_accvgpr_read_b32 %8, a[.Ldsa_acc + 8]\n"
+      "v_accvgpr_read_b32 %9, a[.Ldsa_acc + 9]\n"
+      "v_accvgpr_read_b32 %10, a[.Ldsa_acc + 10]\n"
+      "v_accvgpr_read_b32 %11, a[.Ldsa_acc + 11]\n"
+      "v_accvgpr_read_b32 %12, a[.Ldsa_acc + 12]\n"
+      "v_accvgpr_read_b32 %13, a[.Ldsa_acc + 13]\n"
+      "v_accvgpr_read_b32 %14, a[.Ldsa_acc + 14]\n"
+      "v_accvgpr_read_b32 %15, a[.Ldsa_acc + 15]"
+      : "=v"(t[0]), "=v"(t[1]), "=v"(t[2]), "=v"(t[3]), "=v"(t[4]), "=v"(t[5]), "=v"(t[6]), "=v"(t[7]), "=v"(t[8]),
+        "=v"(t[9]), "=v"(t[10]), "=v"(t[11]), "=v"(t[12]), "=v"(t[13]), "=v"(t[14]), "=v"(t[15])
+      : "i"(16 * DT));
+}
+// max(a, b, c) without the quieting the compiler adds around fmaxf of asm outputs
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// Pins the computation of v ahead of this point of the (volatile) asm stream:
+// without it the compiler sinks the softmax arithmetic past the P.V MFMAs it is
+// meant to hide behind.
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(int& v) { asm volatile("" : "+v"(v)); }
+
+// Wait states between a 16-pass MFMA's write and a VALU / memory read of its
+// result (more than the 18 the ISA requires).
+__device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n s_nop 7\n s_nop 7" ::: "memory"); }
+// VALU write -> MFMA source read.
+__device__ __forceinline__ void valu_to_mfma() { asm volatile("s_nop 3" ::: "memory"); }
+
+// Ring layout of the 4-wave form.  A stage holds 32 keys x d_qk in 1 KB blocks
+// (key group kg = key / 8, chunk group cg = chunk / 8) at (cg * 4 + kg) * 1024.
+// Inside a block, chunk pair cp = (chunk % 8) / 2 owns 256 bytes holding the 8
+// keys' 32-byte pieces of that pair, key k at position k ^ 4 (cp % 2), and the
+// two 16-byte chunks of a piece swapped when kg is odd:
+//   offset = cp * 256 + (k ^ 4 (cp % 2)) * 32 + 16 ((chunk % 2) ^ (kg % 2)).
+// Then (a) one global_load_lds of 64 lanes still fetches 8 whole 128-byte rows,
+// (b) the score A fragments (one chunk of 16 keys per 16-lane group) hit 16
+// distinct 16-byte bank groups, and (c) every 16-lane group of a transposing P.V
+// read takes one contiguous 128-byte tile (4 keys x 16 dims), the dense pattern
+// that ds_read_b64_tr_b16 serves near its peak rate (about 2.8x the rate measured
+// for 4 rows at a 128-byte stride), with the two groups read together in
+// disjoint bank halves.
+__device__ __forceinline__ uint32_t w4_pos(int k, int cc, int kg) {
+  const int cp = cc >> 1;
+  return (uint32_t)(cp * 256 + ((k ^ (4 * (cp & 1))) * 32) + 16 * ((cc & 1) ^ (kg & 1)));
+}
+
+// One 32-bit LDS read issued as inline asm (it joins the counted stream of the
+// kernel's own LDS reads instead of drawing a compiler lgkmcnt(0) wait).
+__device__ __forceinline__ int32_t lds_read_b32(uint32_t addr) {
+  int32_t v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+template <int DQK>
+__global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
+  constexpr int NT = 256;
+  constexpr int KS = DQK / 16;          // score k-steps: 36 (576) or 32 (512)
+  constexpr int NCG = DQK / 64;         // 128-byte chunk groups per KV row: 9 or 8
+  constexpr int STAGE = kKT * DQK * 2;  // bytes per ring stage
+  constexpr int ND = kDV / 32;          // P.V d-tiles
+  static_assert(2 * NCG < 64, "vmcnt range");
+  static_assert(KS >= 23, "the softmax is spread over 23 score MFMAs");
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  int32_t* rows = reinterpret_cast<int32_t*>(smem + kW4Stages * STAGE);
+
+  // ---- workgroup -> (token, head group, split), contiguous (token, split)
+  // ranges per XCD as in the 8-wave form
+  const int bid = blockIdx.x;
+  const int xcd = bid % dsa::kNumXcd, rq = bid / dsa::kNumXcd;
+  const int hg = rq % p.nhg;
+  const int64_t T = (int64_t)p.B * p.S;
+  const int64_t units = T * p.nsplit;
+  const int64_t per_xcd = (units + dsa::kNumXcd - 1) / dsa::kNumXcd;
+  const int64_t x = (int64_t)xcd * per_xcd + rq / p.nhg;
+  if (x >= units || rq / p.nhg >= per_xcd) return;
+  const int64_t token = x / p.nsplit;
+  const int split = (int)(x % p.nsplit);
+  const int b = (int)(token / p.S), s = (int)(token % p.S);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS-DMA bases stay scalar
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int head = hg * kHeadsPerGroup + wave * 32 + l32;
+  const bool head_ok = head < p.H;
+  const bool wave_active = hg * kHeadsPerGroup + wave * 32 < p.H;
+  const int kbeg = split * p.keys_per_split;
+  const int nkeys = max(0, min(p.keys_per_split, p.topk - kbeg));
+
+  // ---- Q^T operand of k-step ks: head l32, dims 16 ks + 8 hh .. + 8.  Loaded
+  // behind the index loads of the list and ahead of their use, so the query
+  // fetch overlaps the row resolution and the first gathers; the first score
+  // MFMA waits for it together with the gathers of step 0.
+  dsa::i32x4 qf[KS];
+  resolve_rows<NT>(p, token, b, s, kbeg, nkeys, rows, tid, [&]() {
+    const uint16_t* qp = p.q + (token * p.H + (head_ok ? head : 0)) * DQK + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const dsa::i32x4*>(qp + 16 * ks);
+  });
+  if (!head_ok) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = dsa::i32x4{0, 0, 0, 0};
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // rows[] written
+  __builtin_amdgcn_s_barrier();                        // ... by every wave
+
+  // ---- gathers: wave w fills key group w (keys 8w .. 8w + 7 of the step) in
+  // every chunk group; 16-byte lane l of a block load writes byte 16 l of the
+  // block, i.e. chunk pair l / 16, key ((l / 2) % 8) ^ 4 (l / 16 % 2), chunk of
+  // the pair (l % 2) ^ (w % 2): each key's whole 128-byte row comes from 8 lanes
+  const int gk = ((lane >> 1) & 7) ^ (4 * ((lane >> 4) & 1));
+  const int gch = 2 * (lane >> 4) + ((lane & 1) ^ (wave & 1));
+  const uint32_t lds0 = (uint32_t)(size_t)(DSA_LDS unsigned char*)smem;
+  const uint32_t rows_lds = lds0 + kW4Stages * STAGE;
+  const int last_key = max(nkeys - 1, 0);
+  // rows[] entry of this lane's gather key in step `step` (clamped inside the list)
+  auto row_read = [&](int step) -> int32_t {
+    return lds_read_b32(rows_lds + 4 * min(step * kKT + 8 * wave + gk, last_key));
+  };
+  auto row_ok = [&](int step, int32_t raw) -> int32_t { return step * kKT + 8 * wave + gk < nkeys ? raw : -1; };
+  // source of this lane's 16-byte loads for row rr (-1: the zero row), by selects
+  const uint16_t* const zero_src = g_zero_row + 8 * gch;
+  const uint16_t* const kv_src = p.kv + 8 * gch;
+  const uint16_t* const kv2_src = (p.kv2 ? p.kv2 : p.kv) + 8 * gch;
+  auto gather_src = [&](int32_t rr) -> const uint16_t* {
+    const uint16_t* base = (rr & dsa::kRowTag2) ? kv2_src : kv_src;
+    const uint16_t* src = base + (int64_t)(rr & ~dsa::kRowTag2) * DQK;
+    return rr >= 0 ? src : zero_src;
+  };
+  auto issue_one = [&](int step, const uint16_t* src, auto C) {
+    constexpr int cg = decltype(C)::value;
+    unsigned char* sb = smem + (step % kW4Stages) * STAGE + wave * 1024;
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + 64 * cg), (DSA_LDS void*)(sb + cg * 4096), 16,
+                                     0, 0);
+  };
+  auto issue = [&](int step, const uint16_t* src) {
+    static_for<0, NCG>([&](auto C) { issue_one(step, src, C); });
+  };
+  // rows[] entry of key l32 of step `step`, for its validity bit (clamped)
+  auto mask_read = [&](int step) -> int32_t { return lds_read_b32(rows_lds + 4 * min(step * kKT + l32, last_key)); };
+  auto mask_of = [&](int step, int32_t raw) -> uint32_t {
+    return (uint32_t)__ballot(step * kKT + l32 < nkeys && raw >= 0);
+  };
+
+  // ---- LDS read addresses (bytes from the start of a stage)
+  // score A fragment of k-step ks: key l32 (block kg = l32 / 8, key l32 % 8),
+  // chunk 2 ks + hh, at kq[ks % 4] + (ks / 4) * 4096
+  uint32_t kq[4];
+  {
+    const int kg = l32 >> 3, kr = l32 & 7;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) kq[e] = kg * 1024 + w4_pos(kr, 2 * e + hh, kg);
+  }
+  // P.V A fragment (d-tile dt, k-step kk), transposing read r (keys +8r): group
+  // g = lane / 16 and lane sl = lane % 16 point at key 16 kk + 8 r + 4 hh + sl / 4,
+  // dims 32 dt + 16 (g % 2) + 4 (sl % 4) .. + 4, at vq[dt % 2][r] + (dt / 2) 4096 + kk 2048
+  uint32_t vq[2][2];
+  {
+    const int g = (lane >> 4) & 3, sl = lane & 15;
+    const int vk = 4 * hh + (sl >> 2);
+#pragma unroll
+    for (int d2 = 0; d2 < 2; ++d2)
+#pragma unroll
+      for (int r2 = 0; r2 < 2; ++r2)
+        vq[d2][r2] = r2 * 1024 + w4_pos(vk, 4 * d2 + 2 * (g & 1) + ((sl & 3) >> 1), r2) + 8 * (sl & 1);
+  }
+
+  // ---- softmax state: lanes l32 and l32 + 32 share head l32
+  float m_ref = -__builtin_inff();
+  float l_run = 0.f;
+  if (p.sink != nullptr && split == 0 && head_ok) {
+    m_ref = p.sink[head] * dsa::kLog2e;
+    l_run = hh == 0 ? 1.f : 0.f;
+  }
+  zero_o();
+
+  // P.V A fragments in flight: fragment f = 2 dt + kk, two transposing reads
+  dsa::i32x2 vfr[kW4VPre][2];
+  auto v_read = [&](uint32_t vbase, auto F) {
+    constexpr int f = decltype(F)::value;
+    constexpr int dt = f >> 1, kk = f & 1;
+    vfr[f % kW4VPre][0] = lds_read_tr16<(dt >> 1) * 4096 + kk * 2048>(vbase + vq[dt & 1][0]);
+    vfr[f % kW4VPre][1] = lds_read_tr16<(dt >> 1) * 4096 + kk * 2048>(vbase + vq[dt & 1][1]);
+  };
+
+  // score product of the step in `sbase`: S^T = K . Q^T over KS k-steps, kW4KPre
+  // fragment reads in flight; hook(IntC<f>) runs after MFMA f.  With VPF the
+  // first kW4VPre P.V fragments (of the stage at `vbase`) are read during the last
+  // score MFMAs, whose K reads are already issued, so the P.V phase starts with
+  // its operands in flight.
+  f32x16 sacc;
+  auto scores = [&](uint32_t sbase, uint32_t vbase, auto VPF, auto&& hook) {
+    constexpr bool vpf = decltype(VPF)::value != 0;
+    static_assert(kW4VPre <= kW4KPre, "the V prefetch uses the K-read slots of the last MFMAs");
+    dsa::i32x4 kfr[kW4KPre];
+    static_for<0, kW4KPre>([&](auto F) {
+      constexpr int f = decltype(F)::value;
+      kfr[f] = lds_read_b128<(f / 4) * 4096>(sbase + kq[f % 4]);
+    });
+    static_for<0, KS>([&](auto F) {
+      constexpr int f = decltype(F)::value;
+      constexpr int ky = (KS - 1 - f) < (kW4KPre - 1) ? (KS - 1 - f) : (kW4KPre - 1);
+      constexpr int tail0 = KS - kW4KPre;  // first MFMA without a K read to issue
+      constexpr int vissued = vpf && f > tail0 ? (f - tail0 < kW4VPre ? f - tail0 : kW4VPre) : 0;
+      lds_wait1<ky + 2 * vissued>(kfr[f % kW4KPre]);
+      const dsa::i32x4 cur = kfr[f % kW4KPre];
+      constexpr int fn = f + kW4KPre;
+      if constexpr (fn < KS) kfr[f % kW4KPre] = lds_read_b128<(fn / 4) * 4096>(sbase + kq[fn % 4]);
+      if constexpr (f == 0) mfma32_v0(sacc, cur, qf[f]);
+      else mfma32_v(sacc, cur, qf[f]);
+      if constexpr (vpf && f >= tail0 && f - tail0 < kW4VPre) v_read(vbase, IntC<f - tail0>{});
+      hook(IntC<f>{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // the softmax of one step (S^T in sacc -> P^T in pn) as 23 pieces: mask, maximum,
+  // reference-maximum update, then one exponential (+ sum, + bf16 packing every
+  // second one) per piece.  A raised reference only records alpha: O is rescaled
+  // once the P.V in flight (the previous step's, on the old reference) is done.
+  float tmax = 0.f, mref = 0.f, alpha = 1.f;
+  bool rescale = false;
+  dsa::i32x4 pp[2], pn[2];  // P^T of the previous step (being multiplied) and of this one
+  auto softmax_piece = [&](uint32_t vmask, auto F) {
+    constexpr int f = decltype(F)::value;
+    if constexpr (f == 0) {
+      // invalid keys (a partial step, -1 or masked indices; rare) score -inf.
+      // Element r of this lane is key 8 (r / 4) + 4 hh + r % 4 of the step.
+      (void)vmask;
+    } else if constexpr (f == 1) {
+      tmax = max3(sacc[0], sacc[1], sacc[2]);
+      tmax = max3(tmax, sacc[3], sacc[4]);
+      pin(tmax);
+    } else if constexpr (f == 2) {
+      tmax = max3(tmax, sacc[5], sacc[6]);
+      tmax = max3(tmax, sacc[7], sacc[8]);
+      pin(tmax);
+    } else if constexpr (f == 3) {
+      tmax = max3(tmax, sacc[9], sacc[10]);
+      tmax = max3(tmax, sacc[11], sacc[12]);
+      pin(tmax);
+    } else if constexpr (f == 4) {
+      tmax = max3(tmax, sacc[13], sacc[14]);
+      tmax = max3(tmax, sacc[15], sacc[15]);
+      pin(tmax);
+    } else if constexpr (f == 5) {
+      tmax = xor32_max(tmax) * p.scale_log2;
+      pin(tmax);
+    } else if constexpr (f == 6) {
+      // m_ref is a reference maximum, raised only when a score passes it by more
+      // than 2^kSlack: probabilities exp2(s - m_ref) may reach 2^kSlack, which fp32
+      // and bf16 carry with unchanged relative precision
+      if (__any(tmax > m_ref + kSlack)) {
+        const float m_new = fmaxf(m_ref, tmax);
+        alpha = m_ref == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+        l_run *= alpha;
+        rescale = __any(alpha != 1.f && m_ref != -__builtin_inff());
+        m_ref = m_new;
+      }
+      mref = m_ref == -__builtin_inff() ? 0.f : m_ref;
+      pin(mref);
+    } else if constexpr (f >= 7 && f < 23) {
+      constexpr int i = f - 7;
+      sacc[i] = __builtin_amdgcn_exp2f(fmaf(sacc[i], p.scale_log2, -mref));
+      l_run += sacc[i];
+      pin(l_run);
+      if constexpr (i & 1) {
+        int w = (int)dsa::pack_bf16x2(sacc[i - 1], sacc[i]);
+        pin(w);
+        pn[i >> 3][(i & 7) >> 1] = w;
+      }
+    }
+  };
+  auto apply_mask = [&](uint32_t vmask) {
+    if (vmask != 0xffffffffu) {
+      const uint32_t m = vmask >> (4 * hh);
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (!((m >> (8 * (r >> 2) + (r & 3))) & 1u)) sacc[r] = -__builtin_inff();
+    }
+  };
+  auto apply_rescale = [&]() {
+    if (rescale) {
+      mfma_drain();
+      scale_o(alpha);
+      rescale = false;
+    }
+  };
+
+  // P.V of the step in `sbase` with P^T = pp: 32 MFMAs (d-tile dt, k-step kk),
+  // fragment f = 2 dt + kk; softmax piece f - 3 of the next step (vmask) after
+  // MFMA f when `with_softmax`.  The first kW4VPre fragments are in flight
+  // already (read by the score loop) unless `fresh`.
+  auto pv = [&](uint32_t sbase, auto with_softmax, uint32_t vmask, bool fresh) {
+    if (fresh) static_for<0, kW4VPre>([&](auto F) { v_read(sbase, F); });
+    static_for<0, 2 * ND>([&](auto F) {
+      constexpr int f = decltype(F)::value;
+      constexpr int dt = f >> 1, kk = f & 1;
+      constexpr int younger = (2 * ND - 1 - f) < (kW4VPre - 1) ? (2 * ND - 1 - f) : (kW4VPre - 1);
+      lds_wait<2 * younger>(vfr[f % kW4VPre][0], vfr[f % kW4VPre][1]);
+      const dsa::i32x4 av = {vfr[f % kW4VPre][0][0], vfr[f % kW4VPre][0][1], vfr[f % kW4VPre][1][0],
+                             vfr[f % kW4VPre][1][1]};
+      constexpr int fn = f + kW4VPre;
+      if constexpr (fn < 2 * ND) {
+        constexpr int dn = fn >> 1, kn = fn & 1;
+        vfr[f % kW4VPre][0] = lds_read_tr16<(dn >> 1) * 4096 + kn * 2048>(sbase + vq[dn & 1][0]);
+        vfr[f % kW4VPre][1] = lds_read_tr16<(dn >> 1) * 4096 + kn * 2048>(sbase + vq[dn & 1][1]);
+      }
+      mfma32_o<dt>(av, pp[kk]);
+      // the score MFMAs of the next step finished at least three MFMAs ago
+      if constexpr (decltype(with_softmax)::value && f >= 3 && f - 3 < 23) softmax_piece(vmask, IntC<f - 3>{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    if constexpr (decltype(with_softmax)::value && 2 * ND - 3 < 23) {
+      static_for<2 * ND - 3, 23>([&](auto F) { softmax_piece(vmask, F); });
+    }
+  };
+
+  const int nsteps = (nkeys + kKT - 1) / kKT;
+  auto gather_wait = [&](int younger) {  // this wave's gathers done but `younger` steps
+    if (younger >= 2) wait_vmcnt<2 * NCG>();
+    else if (younger == 1) wait_vmcnt<NCG>();
+    else wait_vmcnt<0>();
+  };
+
+  // ---- schedule.  Step j: wait for the gathers of step j, then the barrier
+  // (stage j complete in every wave; stage j - 2 released by every wave), the
+  // scores of j with the gathers of step j + 2 issued one chunk group every four
+  // MFMAs (a burst of loads stalls the issuing wave), then the P.V of j - 1 with
+  // the softmax of j in its shadow.  Stages in use at step j: j - 1 (P.V), j
+  // (scores), j + 1 and j + 2 (loading).  The rows[] entries a step needs (its
+  // validity mask, the gather rows two steps ahead) are read one step early,
+  // ahead of the fragment reads whose waits cover them.
+  int32_t row_raw = 0, mask_raw = 0;
+  if (nsteps > 0) {
+    const int32_t r0 = row_read(0), r1 = row_read(1);
+    row_raw = row_read(2);
+    mask_raw = mask_read(0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    issue(0, gather_src(row_ok(0, r0)));
+    if (nsteps > 1) issue(1, gather_src(row_ok(1, r1)));
+  }
+  for (int j = 0; j < nsteps; ++j) {
+    gather_wait(min(1, nsteps - 1 - j));
+    __builtin_amdgcn_s_barrier();
+    const int32_t row_next = row_read(j + 3);
+    const int32_t mask_next = mask_read(j + 1);
+    const uint32_t vmask = mask_of(j, mask_raw);
+    const bool more = j + 2 < nsteps;
+    const uint16_t* src = gather_src(row_ok(j + 2, row_raw));
+    if (wave_active) {
+      auto gathers = [&](auto F) {
+        constexpr int f = decltype(F)::value;
+        if constexpr ((f & 3) == 1 && (f >> 2) < NCG) {
+          if (more) issue_one(j + 2, src, IntC<(f >> 2)>{});
+        }
+      };
+      const uint32_t vbase = lds0 + ((j + kW4Stages - 1) % kW4Stages) * STAGE;  // stage of step j - 1
+      if (j == 0) {
+        scores(lds0, 0u, IntC<0>{}, gathers);
+        mfma_drain();
+        apply_mask(vmask);
+        static_for<0, 23>([&](auto F) { softmax_piece(vmask, F); });
+      } else {
+        scores(lds0 + (j % kW4Stages) * STAGE, vbase, IntC<1>{}, gathers);
+        mfma_drain();
+        apply_mask(vmask);
+        pv(vbase, IntC<1>{}, vmask, false);
+        apply_rescale();
+      }
+      pp[0] = pn[0];
+      pp[1] = pn[1];
+    } else {
+      if (more) issue(j + 2, src);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    row_raw = row_next;
+    mask_raw = mask_next;
+  }
+  if (nsteps > 0 && wave_active) {
+    valu_to_mfma();
+    pv(lds0 + ((nsteps - 1) % kW4Stages) * STAGE, IntC<0>{}, 0u, true);
+  }
+
+  // ---- epilogue: lane (hh, l32) holds O^T[32 dt + 8 (r / 4) + 4 hh + r % 4][head l32]
+  mfma_drain();
+  const float l_tot = xor32_sum(l_run);
+  const bool has = l_tot > 0.f;
+  const float inv = has ? 1.f / l_tot : 0.f;
+  const float lse_v = has ? (m_ref + __builtin_amdgcn_logf(l_tot)) * dsa::kLn2 : -__builtin_inff();
+
+  // O^T leaves through LDS so that every global store writes a whole 1 KB output
+  // row (one head, 64 lanes x 16 bytes) instead of 32 scattered 16-byte pieces.
+  // Wave w's 32 rows sit at w * 32 KB of the (now idle) ring: 8-dim chunk c of
+  // head h at h * 1024 + 16 (c ^ (h % 16)), its two 8-byte halves swapped for
+  // h >= 16, which keeps both the 8-byte writes (32 heads of one half-wave) and
+  // the 16-byte row reads free of bank conflicts.
+  static_assert(32 * kDV * 2 * 4 <= kW4Stages * STAGE, "O staging fits the ring");
+  __syncthreads();  // every wave is done with the ring
+  unsigned char* const ob = smem + wave * (32 * kDV * 2);
+  const int oh_sw = l32 & 15, ohalf = hh ^ ((l32 >> 4) & 1);
+  auto o_put = [&](int c, dsa::i32x2 v) {
+    *reinterpret_cast<dsa::i32x2*>(ob + l32 * (kDV * 2) + 16 * (c ^ oh_sw) + 8 * ohalf) = v;
+  };
+  auto o_flush = [&](uint16_t* rows_out) {  // rows_out: row of this wave's first head
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int nh = min(32, p.H - (hg * kHeadsPerGroup + wave * 32));
+#pragma unroll 8
+    for (int i = 0; i < 32; ++i) {
+      if (i >= nh) break;
+      dsa::i32x4 v = *reinterpret_cast<const dsa::i32x4*>(ob + i * (kDV * 2) + 16 * (lane ^ (i & 15)));
+      if (i & 16) v = dsa::i32x4{v[2], v[3], v[0], v[1]};
+      *reinterpret_cast<dsa::i32x4*>(rows_out + (int64_t)i * kDV + 8 * lane) = v;
+    }
+  };
+  const int64_t head0 = hg * kHeadsPerGroup + wave * 32;  // this wave's first head
+  if (p.nsplit == 1) {
+    static_for<0, ND>([&](auto D) {
+      constexpr int dt = decltype(D)::value;
+      float t[16];
+      read_o<dt>(t);
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        dsa::i32x2 v;
+        v[0] = (int)dsa::pack_bf16x2(t[4 * q4] * inv, t[4 * q4 + 1] * inv);
+        v[1] = (int)dsa::pack_bf16x2(t[4 * q4 + 2] * inv, t[4 * q4 + 3] * inv);
+        o_put(4 * dt + q4, v);
+      }
+    });
+    if (wave_active) o_flush(p.out + (token * p.H + head0) * kDV);
+    if (head_ok && hh == 0 && p.lse) p.lse[token * p.H + head] = lse_v;
+  } else {
+    // fp16 partials scaled by a power of two per (token, head), as the 8-wave form
+    const int64_t prow0 = (token * p.nsplit + split) * p.H;
+    float amax = 0.f;
+    static_for<0, ND>([&](auto D) {
+      float t[16];
+      read_o<decltype(D)::value>(t);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(t[i]));
+    });
+    amax = xor32_max(amax) * inv;
+    int e = 0;
+    if (amax > 0.f) (void)frexpf(amax, &e);
+    const float down = ldexpf(inv, -e);
+    static_for<0, ND>([&](auto D) {
+      constexpr int dt = decltype(D)::value;
+      float t[16];
+      read_o<dt>(t);
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const _Float16 h0 = (_Float16)(t[4 * q4] * down), h1 = (_Float16)(t[4 * q4 + 1] * down);
+        const _Float16 h2 = (_Float16)(t[4 * q4 + 2] * down), h3 = (_Float16)(t[4 * q4 + 3] * down);
+        dsa::i32x2 v;
+        v[0] = (int)((uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16));
+        v[1] = (int)((uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16));
+        o_put(4 * dt + q4, v);
+      }
+    });
+    if (wave_active) o_flush(p.part_o + (prow0 + head0) * kDV);
+    if (head_ok && hh == 0) {
+      p.part_lse[prow0 + head] = lse_v;
+      p.part_scale[prow0 + head] = ldexpf(1.f, e);
+    }
+  }
+}
+
 // Merge split partials: lse = logsumexp_p lse_p, out = sum_p exp(lse_p - lse) out_p.
 // 64 threads per (token, head) row, 8 dims (16 bytes of fp16) each, four rows per
 // block.  The lse, scale and slice of kCombineU splits are all loaded before any
@@ -524,22 +1139,27 @@ int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   return dsa::check_launch("dsa_sparse_mla_fwd");
 }
 
-// Ring depth and workgroup form.  An 8-wave workgroup (256 VGPRs per wave) fills
-// a CU's register file, so it runs alone on its CU: long index lists (prefill)
-// use a 2-stage ring (measured faster than 3 or 4 there), short ones (decode
-// splits, dominated by gather latency) a 3-stage ring (2 % faster than 4).  4-wave workgroups pair up on a CU
-// with 2-stage rings (<= 80 KB of LDS each) and overlap one's prologue and
-// epilogue with the other's steps.
+template <int DQK>
+int launch_mla_w4(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
+  const size_t smem = (size_t)kW4Stages * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split;
+  auto fn = mla_w4_kernel<DQK>;
+  static std::atomic<int> lds_reserved[dsa::kMaxDevices];
+  const int rc = dsa::reserve_lds((const void*)fn, smem, lds_reserved, "sparse_mla");
+  if (rc != dsa::kOk) return rc;
+  hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3(256), smem, stream, p);
+  return dsa::check_launch("dsa_sparse_mla_fwd");
+}
+
+// Workgroup form.  More than 64 heads: the 4-wave, 128-head form (one
+// workgroup per CU, a 4-stage ring, O in the accumulation registers).  64 or
+// fewer heads: 4-wave, 64-head workgroups with 2-stage rings (<= 80 KB of LDS
+// each) that pair up on a CU, so one's prologue and epilogue runs beside the
+// other's steps -- when two of them fit in the CU's 160 KB of LDS.
 template <int DQK>
 int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
-  // 64 or fewer heads: 4-wave workgroups, when two of them fit in a CU's 160 KB
-  // of LDS (not at d_qk = 576 with 2048-key lists: the 128-head form then).
-  // Two 64-head workgroups per CU measured slower than one of 128 heads for H = 128.
   const size_t lds4 = (size_t)kStagesPair * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split + 64;
   if (p.H <= 64 && 2 * lds4 <= 160 * 1024) return launch_mla_stages<DQK, kStagesPair, 4>(p, nblocks, stream);
-  if (nblocks >= 1024 && p.keys_per_split > 512)
-    return launch_mla_stages<DQK, kStagesPair, kWaves>(p, nblocks, stream);
-  return launch_mla_stages<DQK, kStagesWide, kWaves>(p, nblocks, stream);
+  return launch_mla_w4<DQK>(p, nblocks, stream);
 }
 
 int choose_splits(int64_t tokens, int nhg, int topk) {
