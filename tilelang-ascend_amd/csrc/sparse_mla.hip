@@ -614,8 +614,8 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
 // Pins the computation of v ahead of this point of the (volatile) asm stream:
 // without it the compiler sinks the softmax arithmetic past the P.V MFMAs it is
 // meant to hide behind.
-__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
-__device__ __forceinline__ void pin(int& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(float& v) { asm volatile("" ::"v"(v)); }
+__device__ __forceinline__ void pin(int& v) { asm volatile("" ::"v"(v)); }
 
 // Wait states between a 16-pass MFMA's write and a VALU / memory read of its
 // result (more than the 18 the ISA requires).
@@ -786,8 +786,14 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   // first kW4VPre P.V fragments (of the stage at `vbase`) are read during the last
   // score MFMAs, whose K reads are already issued, so the P.V phase starts with
   // its operands in flight.
-  f32x16 sacc;
-  auto scores = [&](uint32_t sbase, uint32_t vbase, auto VPF, auto&& hook) {
+  // Score accumulators and P^T by step parity: the softmax of step j starts in
+  // the shadow of the P.V MFMAs of step j - 1 (its maximum and the first half of
+  // its exponentials) and ends in the shadow of the score MFMAs of step j + 1, so
+  // that neither phase holds more than about eight instructions per 32-cycle
+  // MFMA (the issue rate of one wave).
+  f32x16 sacc[2];
+  dsa::i32x4 pbuf[2][2];  // P^T: the B operands of the two P.V k-steps
+  auto scores = [&](f32x16& acc, uint32_t sbase, uint32_t vbase, auto VPF, auto&& hook) {
     constexpr bool vpf = decltype(VPF)::value != 0;
     static_assert(kW4VPre <= kW4KPre, "the V prefetch uses the K-read slots of the last MFMAs");
     dsa::i32x4 kfr[kW4KPre];
@@ -804,45 +810,45 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
       const dsa::i32x4 cur = kfr[f % kW4KPre];
       constexpr int fn = f + kW4KPre;
       if constexpr (fn < KS) kfr[f % kW4KPre] = lds_read_b128<(fn / 4) * 4096>(sbase + kq[fn % 4]);
-      if constexpr (f == 0) mfma32_v0(sacc, cur, qf[f]);
-      else mfma32_v(sacc, cur, qf[f]);
+      if constexpr (f == 0) mfma32_v0(acc, cur, qf[f]);
+      else mfma32_v(acc, cur, qf[f]);
       if constexpr (vpf && f >= tail0 && f - tail0 < kW4VPre) v_read(vbase, IntC<f - tail0>{});
       hook(IntC<f>{});
       __builtin_amdgcn_sched_barrier(0);
     });
   };
 
-  // the softmax of one step (S^T in sacc -> P^T in pn) as 23 pieces: mask, maximum,
-  // reference-maximum update, then one exponential (+ sum, + bf16 packing every
-  // second one) per piece.  A raised reference only records alpha: O is rescaled
-  // once the P.V in flight (the previous step's, on the old reference) is done.
+  // The softmax of one step (S^T in sc -> P^T in pb).  Pieces 1-6: maximum and
+  // reference-maximum update; pieces 7-23: exponential k = piece - 7 (< 16), then
+  // the sum and bf16 packing of exponential k - 1, so that no instruction reads
+  // the result of the transcendental just before it.  A raised reference only
+  // records alpha: O is rescaled once the P.V in flight (the previous step's, on
+  // the old reference) is done.
+  constexpr int kSoftPieces = 24;  // pieces 1 .. 23
+  constexpr int kSoftSplit = 15;   // pieces < kSoftSplit run beside the P.V MFMAs
   float tmax = 0.f, mref = 0.f, alpha = 1.f;
   bool rescale = false;
-  dsa::i32x4 pp[2], pn[2];  // P^T of the previous step (being multiplied) and of this one
-  auto softmax_piece = [&](uint32_t vmask, auto F) {
+  auto softmax_piece = [&](f32x16& sc, dsa::i32x4 (&pb)[2], auto F) {
     constexpr int f = decltype(F)::value;
-    if constexpr (f == 0) {
-      // invalid keys (a partial step, -1 or masked indices; rare) score -inf.
-      // Element r of this lane is key 8 (r / 4) + 4 hh + r % 4 of the step.
-      (void)vmask;
-    } else if constexpr (f == 1) {
-      tmax = max3(sacc[0], sacc[1], sacc[2]);
-      tmax = max3(tmax, sacc[3], sacc[4]);
+    if constexpr (f == 1) {
+      tmax = max3(sc[0], sc[1], sc[2]);
+      tmax = max3(tmax, sc[3], sc[4]);
       pin(tmax);
     } else if constexpr (f == 2) {
-      tmax = max3(tmax, sacc[5], sacc[6]);
-      tmax = max3(tmax, sacc[7], sacc[8]);
+      tmax = max3(tmax, sc[5], sc[6]);
+      tmax = max3(tmax, sc[7], sc[8]);
       pin(tmax);
     } else if constexpr (f == 3) {
-      tmax = max3(tmax, sacc[9], sacc[10]);
-      tmax = max3(tmax, sacc[11], sacc[12]);
+      tmax = max3(tmax, sc[9], sc[10]);
+      tmax = max3(tmax, sc[11], sc[12]);
       pin(tmax);
     } else if constexpr (f == 4) {
-      tmax = max3(tmax, sacc[13], sacc[14]);
-      tmax = max3(tmax, sacc[15], sacc[15]);
+      tmax = max3(tmax, sc[13], sc[14]);
+      tmax = max3(tmax, sc[15], sc[15]);
       pin(tmax);
     } else if constexpr (f == 5) {
-      tmax = xor32_max(tmax) * p.scale_log2;
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+      tmax = max3(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1])) * p.scale_log2;
       pin(tmax);
     } else if constexpr (f == 6) {
       // m_ref is a reference maximum, raised only when a score passes it by more
@@ -857,24 +863,35 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
       }
       mref = m_ref == -__builtin_inff() ? 0.f : m_ref;
       pin(mref);
-    } else if constexpr (f >= 7 && f < 23) {
-      constexpr int i = f - 7;
-      sacc[i] = __builtin_amdgcn_exp2f(fmaf(sacc[i], p.scale_log2, -mref));
-      l_run += sacc[i];
-      pin(l_run);
-      if constexpr (i & 1) {
-        int w = (int)dsa::pack_bf16x2(sacc[i - 1], sacc[i]);
-        pin(w);
-        pn[i >> 3][(i & 7) >> 1] = w;
+    } else if constexpr (f >= 7 && f < kSoftPieces) {
+      constexpr int k = f - 7;
+      if constexpr (k < 16) {
+        float x = __builtin_amdgcn_exp2f(fmaf(sc[k], p.scale_log2, -mref));
+        pin(x);
+        sc[k] = x;
+      }
+      if constexpr (k >= 1) {
+        l_run += sc[k - 1];
+        pin(l_run);
+        if constexpr ((k - 1) & 1) {
+          int w = (int)dsa::pack_bf16x2(sc[k - 2], sc[k - 1]);
+          pin(w);
+          pb[(k - 1) >> 3][((k - 1) & 7) >> 1] = w;
+        }
       }
     }
   };
-  auto apply_mask = [&](uint32_t vmask) {
+  auto softmax_range = [&](f32x16& sc, dsa::i32x4 (&pb)[2], auto LO, auto HI) {
+    static_for<decltype(LO)::value, decltype(HI)::value>([&](auto F) { softmax_piece(sc, pb, F); });
+  };
+  // invalid keys (a partial step, -1 or masked indices; rare) score -inf.
+  // Element r of this lane is key 8 (r / 4) + 4 hh + r % 4 of the step.
+  auto apply_mask = [&](f32x16& sc, uint32_t vmask) {
     if (vmask != 0xffffffffu) {
       const uint32_t m = vmask >> (4 * hh);
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        if (!((m >> (8 * (r >> 2) + (r & 3))) & 1u)) sacc[r] = -__builtin_inff();
+        if (!((m >> (8 * (r >> 2) + (r & 3))) & 1u)) sc[r] = -__builtin_inff();
     }
   };
   auto apply_rescale = [&]() {
@@ -886,10 +903,9 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   };
 
   // P.V of the step in `sbase` with P^T = pp: 32 MFMAs (d-tile dt, k-step kk),
-  // fragment f = 2 dt + kk; softmax piece f - 3 of the next step (vmask) after
-  // MFMA f when `with_softmax`.  The first kW4VPre fragments are in flight
-  // already (read by the score loop) unless `fresh`.
-  auto pv = [&](uint32_t sbase, auto with_softmax, uint32_t vmask, bool fresh) {
+  // fragment f = 2 dt + kk; hook(IntC<f>) after MFMA f.  The first kW4VPre
+  // fragments are in flight already (read by the score loop) unless `fresh`.
+  auto pv = [&](uint32_t sbase, const dsa::i32x4 (&pp)[2], bool fresh, auto&& hook) {
     if (fresh) static_for<0, kW4VPre>([&](auto F) { v_read(sbase, F); });
     static_for<0, 2 * ND>([&](auto F) {
       constexpr int f = decltype(F)::value;
@@ -905,13 +921,9 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
         vfr[f % kW4VPre][1] = lds_read_tr16<(dn >> 1) * 4096 + kn * 2048>(sbase + vq[dn & 1][1]);
       }
       mfma32_o<dt>(av, pp[kk]);
-      // the score MFMAs of the next step finished at least three MFMAs ago
-      if constexpr (decltype(with_softmax)::value && f >= 3 && f - 3 < 23) softmax_piece(vmask, IntC<f - 3>{});
+      hook(IntC<f>{});
       __builtin_amdgcn_sched_barrier(0);
     });
-    if constexpr (decltype(with_softmax)::value && 2 * ND - 3 < 23) {
-      static_for<2 * ND - 3, 23>([&](auto F) { softmax_piece(vmask, F); });
-    }
   };
 
   const int nsteps = (nkeys + kKT - 1) / kKT;
@@ -924,21 +936,25 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   // ---- schedule.  Step j: wait for the gathers of step j, then the barrier
   // (stage j complete in every wave; stage j - 2 released by every wave), the
   // scores of j with the gathers of step j + 2 issued one chunk group every four
-  // MFMAs (a burst of loads stalls the issuing wave), then the P.V of j - 1 with
-  // the softmax of j in its shadow.  Stages in use at step j: j - 1 (P.V), j
-  // (scores), j + 1 and j + 2 (loading).  The rows[] entries a step needs (its
-  // validity mask, the gather rows two steps ahead) are read one step early,
-  // ahead of the fragment reads whose waits cover them.
+  // MFMAs (a burst of loads stalls the issuing wave) and the second half of the
+  // softmax of j - 1, then the P.V of j - 1 with the first half of the softmax of
+  // j.  Stages in use at step j: j - 1 (P.V), j (scores), j + 1 and j + 2
+  // (loading).  The rows[] entries a step needs (its validity mask, the gather
+  // rows two steps ahead) are read one step early, ahead of the fragment reads
+  // whose waits cover them.  The loop is unrolled by two so that the parity
+  // buffers are registers.
   int32_t row_raw = 0, mask_raw = 0;
   if (nsteps > 0) {
-    const int32_t r0 = row_read(0), r1 = row_read(1);
+    int32_t r0 = row_read(0), r1 = row_read(1);
     row_raw = row_read(2);
     mask_raw = mask_read(0);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // tied to the wait: no use of the four values may be scheduled before it
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r0), "+v"(r1), "+v"(row_raw), "+v"(mask_raw)::"memory");
     issue(0, gather_src(row_ok(0, r0)));
     if (nsteps > 1) issue(1, gather_src(row_ok(1, r1)));
   }
-  for (int j = 0; j < nsteps; ++j) {
+  auto step = [&](int j, auto PAR) {
+    constexpr int P = decltype(PAR)::value, Q = 1 - P;  // buffers of step j and of step j - 1
     gather_wait(min(1, nsteps - 1 - j));
     __builtin_amdgcn_s_barrier();
     const int32_t row_next = row_read(j + 3);
@@ -947,37 +963,71 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
     const bool more = j + 2 < nsteps;
     const uint16_t* src = gather_src(row_ok(j + 2, row_raw));
     if (wave_active) {
-      auto gathers = [&](auto F) {
-        constexpr int f = decltype(F)::value;
-        if constexpr ((f & 3) == 1 && (f >> 2) < NCG) {
-          if (more) issue_one(j + 2, src, IntC<(f >> 2)>{});
-        }
-      };
+      const uint32_t sbase = lds0 + (j % kW4Stages) * STAGE;
       const uint32_t vbase = lds0 + ((j + kW4Stages - 1) % kW4Stages) * STAGE;  // stage of step j - 1
       if (j == 0) {
-        scores(lds0, 0u, IntC<0>{}, gathers);
+        scores(sacc[P], sbase, 0u, IntC<0>{}, [&](auto F) {
+          constexpr int f = decltype(F)::value;
+          if constexpr ((f & 3) == 1 && (f >> 2) < NCG) {
+            if (more) issue_one(j + 2, src, IntC<(f >> 2)>{});
+          }
+        });
         mfma_drain();
-        apply_mask(vmask);
-        static_for<0, 23>([&](auto F) { softmax_piece(vmask, F); });
+        apply_mask(sacc[P], vmask);
+        softmax_range(sacc[P], pbuf[P], IntC<1>{}, IntC<kSoftSplit>{});
       } else {
-        scores(lds0 + (j % kW4Stages) * STAGE, vbase, IntC<1>{}, gathers);
+        // gathers at MFMAs 1, 5, 9, ..; the softmax tail of j - 1 at 3, 7, 11, ..
+        scores(sacc[P], sbase, vbase, IntC<1>{}, [&](auto F) {
+          constexpr int f = decltype(F)::value;
+          if constexpr ((f & 3) == 1 && (f >> 2) < NCG) {
+            if (more) issue_one(j + 2, src, IntC<(f >> 2)>{});
+          }
+          if constexpr ((f & 3) == 3 && kSoftSplit + (f >> 2) < kSoftPieces)
+            softmax_piece(sacc[Q], pbuf[Q], IntC<kSoftSplit + (f >> 2)>{});
+        });
+        // pieces the score MFMAs had no room for (d_qk = 512)
+        constexpr int placed = kSoftSplit + KS / 4 < kSoftPieces ? kSoftSplit + KS / 4 : kSoftPieces;
+        softmax_range(sacc[Q], pbuf[Q], IntC<placed>{}, IntC<kSoftPieces>{});
         mfma_drain();
-        apply_mask(vmask);
-        pv(vbase, IntC<1>{}, vmask, false);
+        apply_mask(sacc[P], vmask);
+        // maximum at MFMAs 3 .. 8, then one exponential every other MFMA
+        pv(vbase, pbuf[Q], false, [&](auto F) {
+          constexpr int f = decltype(F)::value;
+          if constexpr (f >= 3 && f < 9) softmax_piece(sacc[P], pbuf[P], IntC<f - 2>{});
+          if constexpr (f >= 9 && ((f - 9) & 1) == 0 && 7 + (f - 9) / 2 < kSoftSplit)
+            softmax_piece(sacc[P], pbuf[P], IntC<7 + (f - 9) / 2>{});
+        });
+        static_assert(9 + 2 * (kSoftSplit - 8) <= 2 * ND, "the softmax head fits the P.V MFMAs");
         apply_rescale();
       }
-      pp[0] = pn[0];
-      pp[1] = pn[1];
     } else {
       if (more) issue(j + 2, src);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
+    // The two rows[] reads land in their registers asynchronously, after the
+    // fragment waits above; a use here keeps the compiler from handing those
+    // registers to other values before then (in the last steps the entries
+    // themselves are not needed).
+    asm volatile("" ::"v"(row_next), "v"(mask_next));
     row_raw = row_next;
     mask_raw = mask_next;
-  }
-  if (nsteps > 0 && wave_active) {
+  };
+  auto last = [&](auto PAR) {  // the step nsteps - 1 has parity PAR
+    constexpr int P = decltype(PAR)::value;
+    softmax_range(sacc[P], pbuf[P], IntC<kSoftSplit>{}, IntC<kSoftPieces>{});
     valu_to_mfma();
-    pv(lds0 + ((nsteps - 1) % kW4Stages) * STAGE, IntC<0>{}, 0u, true);
+    pv(lds0 + ((nsteps - 1) % kW4Stages) * STAGE, pbuf[P], true, [](auto) {});
+  };
+  if (nsteps > 0) step(0, IntC<0>{});
+  int j = 1;
+  for (; j + 1 < nsteps; j += 2) {
+    step(j, IntC<1>{});
+    step(j + 1, IntC<0>{});
+  }
+  if (j < nsteps) step(j, IntC<1>{});
+  if (nsteps > 0 && wave_active) {
+    if ((nsteps - 1) & 1) last(IntC<1>{});
+    else last(IntC<0>{});
   }
 
   // ---- epilogue: lane (hh, l32) holds O^T[32 dt + 8 (r / 4) + 4 hh + r % 4][head l32]
