@@ -725,11 +725,14 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
     const uint16_t* src = base + (int64_t)(rr & ~dsa::kRowTag2) * DQK;
     return rr >= 0 ? src : zero_src;
   };
+  // The instruction's immediate offset (128 cg bytes) applies to both the global
+  // and the LDS address, so the LDS base passed in is pre-biased by -128 cg: one
+  // scalar add for M0 and no per-load address arithmetic.
   auto issue_one = [&](int step, const uint16_t* src, auto C) {
     constexpr int cg = decltype(C)::value;
     unsigned char* sb = smem + (step % kW4Stages) * STAGE + wave * 1024;
-    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + 64 * cg), (DSA_LDS void*)(sb + cg * 4096), 16,
-                                     0, 0);
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (DSA_LDS void*)(sb + cg * (4096 - 128)), 16,
+                                     128 * cg, 0);
   };
   auto issue = [&](int step, const uint16_t* src) {
     static_for<0, NCG>([&](auto C) { issue_one(step, src, C); });
@@ -960,17 +963,17 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
     const int32_t row_next = row_read(j + 3);
     const int32_t mask_next = mask_read(j + 1);
     const uint32_t vmask = mask_of(j, mask_raw);
+    // the last two steps load the zero row into idle stages instead of branching
+    // around each load
     const bool more = j + 2 < nsteps;
-    const uint16_t* src = gather_src(row_ok(j + 2, row_raw));
+    const uint16_t* src = more ? gather_src(row_ok(j + 2, row_raw)) : zero_src;
     if (wave_active) {
       const uint32_t sbase = lds0 + (j % kW4Stages) * STAGE;
       const uint32_t vbase = lds0 + ((j + kW4Stages - 1) % kW4Stages) * STAGE;  // stage of step j - 1
       if (j == 0) {
         scores(sacc[P], sbase, 0u, IntC<0>{}, [&](auto F) {
           constexpr int f = decltype(F)::value;
-          if constexpr ((f & 3) == 1 && (f >> 2) < NCG) {
-            if (more) issue_one(j + 2, src, IntC<(f >> 2)>{});
-          }
+          if constexpr ((f & 3) == 1 && (f >> 2) < NCG) issue_one(j + 2, src, IntC<(f >> 2)>{});
         });
         mfma_drain();
         apply_mask(sacc[P], vmask);
@@ -979,9 +982,7 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
         // gathers at MFMAs 1, 5, 9, ..; the softmax tail of j - 1 at 3, 7, 11, ..
         scores(sacc[P], sbase, vbase, IntC<1>{}, [&](auto F) {
           constexpr int f = decltype(F)::value;
-          if constexpr ((f & 3) == 1 && (f >> 2) < NCG) {
-            if (more) issue_one(j + 2, src, IntC<(f >> 2)>{});
-          }
+          if constexpr ((f & 3) == 1 && (f >> 2) < NCG) issue_one(j + 2, src, IntC<(f >> 2)>{});
           if constexpr ((f & 3) == 3 && kSoftSplit + (f >> 2) < kSoftPieces)
             softmax_piece(sacc[Q], pbuf[Q], IntC<kSoftSplit + (f >> 2)>{});
         });
@@ -1001,7 +1002,7 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
         apply_rescale();
       }
     } else {
-      if (more) issue(j + 2, src);
+      issue(j + 2, src);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     // The two rows[] reads land in their registers asynchronously, after the
