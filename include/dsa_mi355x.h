@@ -168,6 +168,24 @@ int dsa_lightning_indexer_fp8_varlen(const void* q, const void* k, const float* 
                                      size_t workspace_bytes, void* stream);
 
 /*
+ * The same full indexer for the reference wrapper's own input dtypes: q
+ * [q_rows, N1, 128] and k fp16 (is_f16 = 1) or bf16 (0), 1 <= N1 <= 64 heads,
+ * weights [q_rows, N1] fp32 (lightning_indexer.py:1250-1255, 1284-1285).  q.k
+ * accumulates the exact 16-bit products in fp32 (16-bit MFMA), as the golden
+ * cpu_lightning_indexer computes in fp32 (:272-305).  key_scale (per key row) is
+ * optional, as above; layouts, lengths, outputs and workspace as
+ * dsa_lightning_indexer_fp8_varlen.  q and k must be 16-byte aligned.
+ */
+int dsa_lightning_indexer_h16_varlen(const void* q, const void* k, const float* key_scale,
+                                     const float* weights, const int32_t* seq_q, int32_t seq_q_cumulative,
+                                     const int32_t* seq_k, int32_t seq_k_cumulative,
+                                     const int32_t* block_table, int32_t block_size, int32_t max_blocks,
+                                     int64_t pool_rows, int64_t B, int64_t S1, int64_t S2, int64_t q_rows,
+                                     int32_t N1, int32_t D, int32_t is_f16, int32_t sparse_count,
+                                     int32_t sparse_mode, int32_t* indices, float* values, void* workspace,
+                                     size_t workspace_bytes, void* stream);
+
+/*
  * Sparse MLA forward: bf16 q [B, S, H, d_qk], one latent KV head, d_v = 512.
  * Replaces the `call` of sparse_attention_fwd
  * (examples/sparse_flash_attention/example_sparse_flash_attn.py:18-243, main(Q, KV,
@@ -196,6 +214,21 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices,
                        int32_t topk, float sm_scale, int32_t is_causal, int32_t num_splits,
                        void* out, float* lse, void* workspace, size_t workspace_bytes,
                        void* stream);
+
+/*
+ * dsa_sparse_mla_fwd for fp16 q / kv, out [B, S, H, 512] fp16 (fp16 MFMA, the
+ * probabilities rounded to fp16 before P.V).  Replaces the same calls as
+ * dsa_sparse_mla_fwd built for the reference factory's default dtype, fp16
+ * (examples/sparse_flash_attention/example_sparse_flash_attn.py:49, output
+ * cast :292, driver :296).  Same arguments, rules and workspace otherwise.
+ */
+int dsa_sparse_mla_fwd_f16(const void* q, const void* kv, const int32_t* indices,
+                           const int32_t* block_table, const int32_t* kv_len, const int32_t* q_start,
+                           const float* attn_sink, int64_t B, int64_t S, int32_t H, int32_t d_qk,
+                           int32_t d_v, int64_t skv, int32_t block_size, int32_t max_blocks,
+                           int32_t topk, float sm_scale, int32_t is_causal, int32_t num_splits,
+                           void* out, float* lse, void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 /*
  * dsa_sparse_mla_fwd without a workspace argument and without any allocation.
@@ -269,6 +302,19 @@ int dsa_sparse_flash_mla(const void* q, int64_t T, int32_t N1, int32_t D, const 
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * dsa_sparse_flash_mla for fp16 q / ori_kv / cmp_kv and an fp16 out (the API's
+ * fp16 mapping, sparse_flash_mla_api.py:16-21).  Same arguments otherwise.
+ */
+int dsa_sparse_flash_mla_f16(const void* q, int64_t T, int32_t N1, int32_t D, const int32_t* q_prefix,
+                             const int32_t* act_q_lens, const int32_t* seqused_kv, int64_t B, const void* ori_kv,
+                             int64_t ori_blocks, int32_t ori_block_size, const int32_t* ori_block_table,
+                             int32_t ori_table_len, const void* cmp_kv, int64_t cmp_blocks, int32_t cmp_block_size,
+                             const int32_t* cmp_block_table, int32_t cmp_table_len,
+                             const int32_t* cmp_sparse_indices, int32_t topk_cmp, int32_t n_cmp, int32_t cmp_ratio,
+                             const float* sinks, float softmax_scale, int32_t ori_win_left, void* out, float* lse,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Row quantisation (the step before the indexer).  x is bf16 [rows, cols],
  * cols a multiple of 8, x 16-byte and y 8-byte aligned; one scale per row.
  *
@@ -307,6 +353,15 @@ int dsa_indexer_k_append_fp8(const void* k, int64_t T, int32_t D, const int64_t*
  */
 int dsa_indexer_q_quant_fp8(const void* q, const float* weights, int64_t T, int32_t N1, int32_t D,
                             void* q8, float* weights_out, void* stream);
+
+/*
+ * dsa_quant_fp8_rows and dsa_indexer_q_quant_fp8 for fp16 inputs (same rules,
+ * same outputs).  They let the lightning indexer take the reference's fp16 q / k
+ * (lightning_indexer.py:1250-1255) by quantising them on the device.
+ */
+int dsa_quant_fp8_rows_f16(const void* x, int64_t rows, int64_t cols, void* y, float* scale, void* stream);
+int dsa_indexer_q_quant_fp8_f16(const void* q, const float* weights, int64_t T, int32_t N1, int32_t D,
+                                void* q8, float* weights_out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -64,15 +64,17 @@ def test_long_list_prefill_form(gpu):
     assert torch.equal(o2.cpu(), out[:, t].cpu()) and torch.equal(l2.cpu(), lse[:, t].cpu())
 
 
-def test_reference_example_case(gpu):
-    # example_sparse_flash_attn.py:295-326 in bf16: B=1, S=128, SKV=32768, H=128,
-    # topk=2048, q_start = 4096 * 7, q, kv ~ N(0, 1), row t draws
-    # randperm(t + q_start)[:topk], padded with the sentinel SKV (none needed here)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_reference_example_case(gpu, dtype):
+    # example_sparse_flash_attn.py:295-326: B=1, S=128, SKV=32768, H=128, topk=2048,
+    # q_start = 4096 * 7, q, kv ~ N(0, 1) in the example's fp16 (:297) and in bf16,
+    # row t draws randperm(t + q_start)[:topk], padded with the sentinel SKV (none
+    # needed here)
     B, S, SKV, topk, q_start = 1, 128, 32768, 2048, 4096 * 7
-    _say(f"reference example case S={S} SKV={SKV} topk={topk} q_start={q_start}")
+    _say(f"reference example case {dtype} S={S} SKV={SKV} topk={topk} q_start={q_start}")
     g = torch.Generator().manual_seed(0)
-    q = torch.randn((B, S, H, DQK), generator=g).to(torch.bfloat16)
-    kv = torch.randn((B, SKV, 1, DQK), generator=g).to(torch.bfloat16)
+    q = torch.randn((B, S, H, DQK), generator=g).to(dtype)
+    kv = torch.randn((B, SKV, 1, DQK), generator=g).to(dtype)
     idx = torch.full((B, S, 1, topk), SKV, dtype=torch.int32)
     for t in range(S):
         i_i = torch.randperm(max(1, t + q_start), generator=g)[:topk]
@@ -80,7 +82,8 @@ def test_reference_example_case(gpu):
     kern = dsa.sparse_attention_fwd(heads=H, dim=512, tail_dim=64, topk=topk, kv_stride=1)
     out = kern(q.to(gpu), kv.to(gpu), idx.to(gpu))
     torch.cuda.synchronize()
-    ro, _ = sparse_mla_fwd_gather(q, kv, idx, None, q_start_index_s=q_start, is_causal=True, p_dtype=torch.bfloat16)
+    assert out.dtype == dtype
+    ro, _ = sparse_mla_fwd_gather(q, kv, idx, None, q_start_index_s=q_start, is_causal=True, p_dtype=dtype)
     # the reference's own assertion is rtol = atol = 1e-2 (:326)
     torch.testing.assert_close(out.float().cpu(), ro, rtol=1e-2, atol=1e-2)
 

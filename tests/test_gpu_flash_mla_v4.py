@@ -35,7 +35,7 @@ def _reference(case):
     S = max(lens)
     kvl = case["seqused_kv"].tolist()
     T, N1, D = case["q"].shape
-    q_bnsd = torch.zeros((B, N1, S, D), dtype=torch.bfloat16)
+    q_bnsd = torch.zeros((B, N1, S, D), dtype=case["q"].dtype)
     for b in range(B):
         q_bnsd[b, :, :lens[b]] = case["q"][cu[b]:cu[b + 1]].permute(1, 0, 2)
     ori = unpack_pages(case["ori_kv"], case["ori_block_table"], max(kvl))
@@ -79,9 +79,14 @@ def _run(case, gpu, layout_q="TND"):
 
 def _check(case, gpu, layout_q="TND"):
     out, lse = _run(case, gpu, layout_q)
+    assert out.dtype == case["q"].dtype
     ro, rl = _reference(case)
-    _contract(out, ro, 0.0078125, 0.0001)
-    _contract(lse, rl, 0.015, 0.005)
+    if case["q"].dtype == torch.bfloat16:  # check_result / check_lse, sparse_flash_mla_golden.py:606-663
+        _contract(out, ro, 0.0078125, 0.0001)
+        _contract(lse, rl, 0.015, 0.005)
+    else:
+        _contract(out, ro, 0.005, 0.000025)
+        _contract(lse, rl, 0.01, 0.001)
     # and no element outside the contract's share is far off: within 1 % of the
     # output range (values here are up to 10; bf16 steps there are 2^-4)
     scale = float(ro.float().abs().max())
@@ -94,6 +99,18 @@ def test_reference_fast_scenarios(gpu, name, scenario, cmp_ratio):
     # FAST_SCENARIOS of sparse_flash_mla_golden.py:384-461: B=1, S=1024, N1=64, D=512, K=512
     case = inputs.flash_mla_v4(scenario=scenario, cmp_ratio=cmp_ratio, seed=42)
     print(f"flash mla v4 {name}", flush=True)
+    _check(case, gpu)
+
+
+@pytest.mark.parametrize("name,scenario,cmp_ratio", [("swa", 1, 4), ("hca", 2, 128), ("csa", 3, 4)])
+def test_reference_fast_scenarios_fp16(gpu, name, scenario, cmp_ratio):
+    # the same cases in fp16, the other dtype the API maps (sparse_flash_mla_api.py:16-21),
+    # under check_result / check_lse's fp16 tolerances; the bf16 inputs convert exactly
+    case = inputs.flash_mla_v4(scenario=scenario, cmp_ratio=cmp_ratio, seed=42)
+    for k in ("q", "ori_kv", "cmp_kv"):
+        if case[k] is not None:
+            case[k] = case[k].to(torch.float16)
+    print(f"flash mla v4 fp16 {name}", flush=True)
     _check(case, gpu)
 
 

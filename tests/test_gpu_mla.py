@@ -170,3 +170,40 @@ def test_sparse_attn_tilelang_signature(gpu, rope, T, act_q):
                                   q_start_index_s=act_kv - act_q, is_causal=True, p_dtype=torch.bfloat16)
     torch.testing.assert_close(out[:act_q].float().cpu(), ro[0], **OUT_TOL)
     assert not out[act_q:].any()
+
+
+@pytest.mark.parametrize("H,splits", [(128, 1), (128, 4), (64, 2), (16, 1)])
+def test_fp16_forms(gpu, H, splits):
+    # fp16 q / kv through both workgroup forms (H > 64: 32-head waves; H <= 64:
+    # paired 64-head workgroups), with and without split partials; the oracle
+    # rounds P to fp16 as the reference golden does (p.type(v.dtype))
+    inp = inputs.mla_prefill(B=2, S=8, Skv=2048, H=H, topk=1024, seed=21)
+    q, kv = inp["q"].to(torch.float16), inp["kv"].to(torch.float16)
+    print(f"mla fp16 H={H} splits={splits}", flush=True)
+    out, lse = dsa.sparse_mla_fwd(q.to(gpu), kv.to(gpu), inp["indices"].to(gpu), inp["sm_scale"], num_splits=splits)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16
+    ro, rl = sparse_mla_fwd_gather(q, kv, inp["indices"], inp["sm_scale"], p_dtype=torch.float16)
+    torch.testing.assert_close(out.float().cpu(), ro, **OUT_TOL)
+    torch.testing.assert_close(lse.cpu(), rl, **LSE_TOL)
+
+
+def test_fp16_paged_decode(gpu):
+    inp = inputs.mla_decode(B=4, ctx=4096, H=128, topk=512, block_size=64, seed=22)
+    q, kv = inp["q"].to(torch.float16), inp["kv"].to(torch.float16)
+    print("mla fp16 paged decode", flush=True)
+    out, lse = dsa.sparse_mla_fwd(q.to(gpu), kv.to(gpu), inp["indices"].to(gpu), inp["sm_scale"],
+                                  block_table=inp["block_table"].to(gpu), seq_len_kv=inp["seq_len_kv"].to(gpu),
+                                  is_causal=False)
+    torch.cuda.synchronize()
+    ro, rl = sparse_mla_fwd_gather(q, kv, inp["indices"], inp["sm_scale"], block_table=inp["block_table"],
+                                   p_dtype=torch.float16)
+    torch.testing.assert_close(out.float().cpu(), ro, **OUT_TOL)
+    torch.testing.assert_close(lse.cpu(), rl, **LSE_TOL)
+
+
+def test_mixed_dtypes_rejected(gpu):
+    inp = inputs.mla_prefill(B=1, S=4, Skv=256, H=16, topk=64, seed=23)
+    with pytest.raises(ValueError, match="both"):
+        dsa.sparse_mla_fwd(inp["q"].to(gpu), inp["kv"].to(gpu).to(torch.float16), inp["indices"].to(gpu))
+

@@ -35,6 +35,7 @@ enum Code : int {
 };
 
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8;
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
 typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
@@ -56,6 +57,24 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const bf16x2_t v = __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t);
   return __builtin_bit_cast(uint32_t, v);
+}
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+
+// fp32 -> fp16 (round to nearest even) for two values, low half = lo
+// (one v_cvt_pk_f16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  const f16x2_t v = __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Two fp32 values packed as the 16-bit element type of the MLA kernels (F16:
+// IEEE half, else bfloat16).
+template <bool F16>
+__device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
+  if constexpr (F16) return pack_f16x2(lo, hi);
+  else return pack_bf16x2(lo, hi);
 }
 
 __device__ __forceinline__ uint16_t f32_to_bf16(float x) {

@@ -89,8 +89,8 @@ __device__ __forceinline__ int32_t v4_row(const V4Keys& v, int64_t t, int b, int
 #endif
 
 struct MlaRun {
-  const void* q;               // bf16 [B * S, H, d_qk]
-  const void* kv;              // bf16 rows [*, d_qk] (batch rows, a page pool, or pool 1)
+  const void* q;               // [B * S, H, d_qk], bf16 (fp16 when f16)
+  const void* kv;              // rows [*, d_qk] (batch rows, a page pool, or pool 1), q's type
   const int32_t* indices;      // [B * S, topk]
   const int32_t* block_table;  // [B, max_blocks] or null
   const int32_t* kv_len;       // [B] or null
@@ -106,6 +106,7 @@ struct MlaRun {
   int32_t block_size, max_blocks, topk;
   float sm_scale;
   int32_t is_causal, num_splits;
+  int32_t f16;                 // q, kv and out are IEEE half instead of bfloat16
   void* out;
   float* lse;
   void* workspace;

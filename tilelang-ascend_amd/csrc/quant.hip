@@ -1,7 +1,8 @@
 // Row quantisation on gfx950: the producer of the indexer's fp8 operands and the
 // int8 activation quantiser of the DeepSeek-V4 examples.
 //
-// Every row of bf16 x is scaled by its own absolute maximum:
+// Every row of x (bf16, or fp16 through the _f16 entry points) is scaled by its
+// own absolute maximum:
 //   fp8  : s = max(absmax / 448, FLT_MIN),            y = e4m3fn(x / s)
 //   int8 : s = max(absmax, 1e-4) / 127,               y = rne(clamp(x / s, +-127))
 //   int8 with power-of-two scales: s = 2^ceil(log2(max(absmax, 1e-4) / 127)).
@@ -37,7 +38,7 @@ constexpr int kThreads = 256;
 constexpr int kCache = 8;  // 16-byte steps per lane kept in registers
 
 struct QuantArgs {
-  const uint16_t* x;        // bf16 [rows, ld_x]
+  const uint16_t* x;        // bf16 or fp16 [rows, ld_x]
   int64_t rows, cols, ld_x;
   const int64_t* dst_rows;  // [rows] or null (row r -> r)
   int64_t dst_capacity;     // rows of y / scale
@@ -47,15 +48,25 @@ struct QuantArgs {
   const float* fold;        // [rows] or null: scale[dst] = fold[r] * s
 };
 
-__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+// The two 16-bit inputs of a dword as fp32 (exact for both types).
+template <bool F16>
+__device__ __forceinline__ float in_lo(uint32_t w) {
+  if constexpr (F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  else return __uint_as_float(w << 16);
+}
+template <bool F16>
+__device__ __forceinline__ float in_hi(uint32_t w) {
+  if constexpr (F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  else return __uint_as_float(w & 0xffff0000u);
+}
 
+template <bool F16>
 __device__ __forceinline__ float absmax8(const dsa::i32x4& v) {
   float m = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t w = (uint32_t)v[i];
-    m = fmaxf(m, fmaxf(fabsf(bf16_lo(w)), fabsf(bf16_hi(w))));
+    m = fmaxf(m, fmaxf(fabsf(in_lo<F16>(w)), fabsf(in_hi<F16>(w))));
   }
   return m;
 }
@@ -97,11 +108,11 @@ __device__ __forceinline__ float row_scale(float amax) {
   }
 }
 
-template <int MODE>
+template <int MODE, bool F16>
 __device__ __forceinline__ void store8(uint8_t* dst, const dsa::i32x4& v, float s) {
   const uint32_t w0 = (uint32_t)v[0], w1 = (uint32_t)v[1], w2 = (uint32_t)v[2], w3 = (uint32_t)v[3];
-  const uint32_t lo = quant4<MODE>(bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1), s);
-  const uint32_t hi = quant4<MODE>(bf16_lo(w2), bf16_hi(w2), bf16_lo(w3), bf16_hi(w3), s);
+  const uint32_t lo = quant4<MODE>(in_lo<F16>(w0), in_hi<F16>(w0), in_lo<F16>(w1), in_hi<F16>(w1), s);
+  const uint32_t hi = quant4<MODE>(in_lo<F16>(w2), in_hi<F16>(w2), in_lo<F16>(w3), in_hi<F16>(w3), s);
   *reinterpret_cast<dsa::i32x2*>(dst) = dsa::i32x2{(int)lo, (int)hi};
 }
 
@@ -109,7 +120,7 @@ __device__ __forceinline__ void store8(uint8_t* dst, const dsa::i32x4& v, float 
 // group takes R rows, 64 / LPR rows apart (so every load instruction of a wave
 // reads 64 / LPR consecutive rows), and issues all R loads before reducing any,
 // to keep enough bytes in flight per CU.
-template <int LPR, int MODE, int R>
+template <int LPR, int MODE, int R, bool F16>
 __global__ __launch_bounds__(kThreads) void quant_short_rows_kernel(QuantArgs a) {
   constexpr int kRowsPerWave = 64 / LPR;
   const int lane = threadIdx.x & 63;
@@ -137,12 +148,12 @@ __global__ __launch_bounds__(kThreads) void quant_short_rows_kernel(QuantArgs a)
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    float amax = absmax8(v[r]);
+    float amax = absmax8<F16>(v[r]);
 #pragma unroll
     for (int off = LPR / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
     const float s = row_scale<MODE>(amax);
     if (drow[r] >= 0) {
-      if (col_ok) store8<MODE>(a.y + drow[r] * a.ld_y + col, v[r], s);
+      if (col_ok) store8<MODE, F16>(a.y + drow[r] * a.ld_y + col, v[r], s);
       if (sl == 0) {
         const int64_t row = base + (int64_t)r * kRowsPerWave;
         a.scale[drow[r]] = a.fold ? a.fold[row] * s : s;
@@ -151,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void quant_short_rows_kernel(QuantArgs a)
   }
 }
 
-template <int LPR, int MODE>
+template <int LPR, int MODE, bool F16>
 __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
   constexpr int kRowsPerWave = 64 / LPR;
   const int lane = threadIdx.x & 63;
@@ -175,12 +186,12 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
     cache[c] = dsa::i32x4{0, 0, 0, 0};
     if (c < steps && live && col < a.cols) {
       cache[c] = xr[col / 8];
-      amax = fmaxf(amax, absmax8(cache[c]));
+      amax = fmaxf(amax, absmax8<F16>(cache[c]));
     }
   }
   for (int c = kCache; c < steps; ++c) {
     const int64_t col = ((int64_t)c * LPR + sl) * 8;
-    if (live && col < a.cols) amax = fmaxf(amax, absmax8(xr[col / 8]));
+    if (live && col < a.cols) amax = fmaxf(amax, absmax8<F16>(xr[col / 8]));
   }
 #pragma unroll
   for (int off = LPR / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
@@ -190,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
 
   // pass 2: scale, round, store 8 bytes per lane and step
   uint8_t* yr = a.y + drow * a.ld_y;
-  auto emit = [&](int c, const dsa::i32x4& v) { store8<MODE>(yr + ((int64_t)c * LPR + sl) * 8, v, s); };
+  auto emit = [&](int c, const dsa::i32x4& v) { store8<MODE, F16>(yr + ((int64_t)c * LPR + sl) * 8, v, s); };
 #pragma unroll
   for (int c = 0; c < kCache; ++c) {
     const int64_t col = ((int64_t)c * LPR + sl) * 8;
@@ -203,21 +214,21 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(QuantArgs a) {
   if (sl == 0) a.scale[drow] = a.fold ? a.fold[row] * s : s;
 }
 
-template <int MODE, int R>
+template <int MODE, int R, bool F16>
 int launch_short(const QuantArgs& a, int lpr, hipStream_t st, const char* what) {
   const int64_t rows_per_block = (kThreads / 64) * (64 / lpr) * R;
   const int64_t grid = (a.rows + rows_per_block - 1) / rows_per_block;
   if (grid > 0x7fffffff) return dsa::set_error(dsa::kInvalidArgument, "%s: too many rows", what);
   switch (lpr) {
-    case 8: quant_short_rows_kernel<8, MODE, R><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
-    case 16: quant_short_rows_kernel<16, MODE, R><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
-    case 32: quant_short_rows_kernel<32, MODE, R><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
-    default: quant_short_rows_kernel<64, MODE, R><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
+    case 8: quant_short_rows_kernel<8, MODE, R, F16><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
+    case 16: quant_short_rows_kernel<16, MODE, R, F16><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
+    case 32: quant_short_rows_kernel<32, MODE, R, F16><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
+    default: quant_short_rows_kernel<64, MODE, R, F16><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
   }
   return dsa::check_launch(what);
 }
 
-template <int MODE>
+template <int MODE, bool F16>
 int launch_mode(const QuantArgs& a, hipStream_t st, const char* what) {
   int lpr = 8;
   while (lpr < 64 && (int64_t)lpr * 8 < a.cols) lpr *= 2;
@@ -225,22 +236,22 @@ int launch_mode(const QuantArgs& a, hipStream_t st, const char* what) {
     // one load per lane and row; R rows per lane group: 2 up to 2^25 elements
     // (128K-key cache 15.4 -> 12.9 us, 4096-token query 25.0 -> 21.6 us against 4),
     // 4 above (1M rows: 73.9 us against 78.8)
-    if (a.rows * a.cols <= ((int64_t)1 << 25)) return launch_short<MODE, 2>(a, lpr, st, what);
-    return launch_short<MODE, 4>(a, lpr, st, what);
+    if (a.rows * a.cols <= ((int64_t)1 << 25)) return launch_short<MODE, 2, F16>(a, lpr, st, what);
+    return launch_short<MODE, 4, F16>(a, lpr, st, what);
   }
   const int64_t rows_per_block = (kThreads / 64) * (64 / lpr);
   const int64_t grid = (a.rows + rows_per_block - 1) / rows_per_block;
   if (grid > 0x7fffffff) return dsa::set_error(dsa::kInvalidArgument, "%s: too many rows", what);
   switch (lpr) {
-    case 8: quant_rows_kernel<8, MODE><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
-    case 16: quant_rows_kernel<16, MODE><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
-    case 32: quant_rows_kernel<32, MODE><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
-    default: quant_rows_kernel<64, MODE><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
+    case 8: quant_rows_kernel<8, MODE, F16><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
+    case 16: quant_rows_kernel<16, MODE, F16><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
+    case 32: quant_rows_kernel<32, MODE, F16><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
+    default: quant_rows_kernel<64, MODE, F16><<<(unsigned)grid, kThreads, 0, st>>>(a); break;
   }
   return dsa::check_launch(what);
 }
 
-int quant_launch(int mode, const QuantArgs& a, void* stream, const char* what) {
+int quant_launch(int mode, const QuantArgs& a, void* stream, const char* what, bool f16 = false) {
   if (a.rows < 0 || a.cols <= 0 || a.cols % 8 != 0 || a.ld_x < a.cols || a.ld_x % 8 != 0 ||
       a.ld_y < a.cols || a.ld_y % 8 != 0)
     return dsa::set_error(dsa::kInvalidArgument,
@@ -253,10 +264,11 @@ int quant_launch(int mode, const QuantArgs& a, void* stream, const char* what) {
   if ((reinterpret_cast<uintptr_t>(a.x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(a.y) & 7u) != 0)
     return dsa::set_error(dsa::kInvalidArgument, "%s: x must be 16-byte and y 8-byte aligned", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (f16) return launch_mode<kFp8, true>(a, st, what);  // fp16 inputs: the fp8 producers only
   switch (mode) {
-    case kFp8: return launch_mode<kFp8>(a, st, what);
-    case kInt8: return launch_mode<kInt8>(a, st, what);
-    default: return launch_mode<kInt8Pow2>(a, st, what);
+    case kFp8: return launch_mode<kFp8, false>(a, st, what);
+    case kInt8: return launch_mode<kInt8, false>(a, st, what);
+    default: return launch_mode<kInt8Pow2, false>(a, st, what);
   }
 }
 
@@ -297,4 +309,23 @@ extern "C" int dsa_indexer_q_quant_fp8(const void* q, const float* weights, int6
   QuantArgs a{static_cast<const uint16_t*>(q), T * N1, D, D, nullptr, T * N1, static_cast<uint8_t*>(q8), D,
               weights_out, weights};
   return quant_launch(kFp8, a, stream, "dsa_indexer_q_quant_fp8");
+}
+
+extern "C" int dsa_quant_fp8_rows_f16(const void* x, int64_t rows, int64_t cols, void* y, float* scale,
+                                      void* stream) {
+  QuantArgs a{static_cast<const uint16_t*>(x), rows, cols, cols, nullptr, rows,
+              static_cast<uint8_t*>(y), cols, scale, nullptr};
+  return quant_launch(kFp8, a, stream, "dsa_quant_fp8_rows_f16", true);
+}
+
+extern "C" int dsa_indexer_q_quant_fp8_f16(const void* q, const float* weights, int64_t T, int32_t N1, int32_t D,
+                                           void* q8, float* weights_out, void* stream) {
+  if (N1 <= 0 || T < 0)
+    return dsa::set_error(dsa::kInvalidArgument, "dsa_indexer_q_quant_fp8_f16: bad sizes (T %lld, N1 %d)",
+                          (long long)T, N1);
+  if (T > 0 && weights == nullptr)
+    return dsa::set_error(dsa::kInvalidArgument, "dsa_indexer_q_quant_fp8_f16: null weights");
+  QuantArgs a{static_cast<const uint16_t*>(q), T * N1, D, D, nullptr, T * N1, static_cast<uint8_t*>(q8), D,
+              weights_out, weights};
+  return quant_launch(kFp8, a, stream, "dsa_indexer_q_quant_fp8_f16", true);
 }

@@ -27,17 +27,17 @@ extern "C" size_t dsa_sparse_flash_mla_workspace_bytes(int64_t T, int32_t N1, in
   return dsa::sparse_mla_split_bytes(T, N1, ori_win_left + 1 + n_cmp, 0);
 }
 
-extern "C" int dsa_sparse_flash_mla(const void* q, int64_t T, int32_t N1, int32_t D, const int32_t* q_prefix,
-                                    const int32_t* act_q_lens, const int32_t* seqused_kv, int64_t B,
-                                    const void* ori_kv, int64_t ori_blocks, int32_t ori_block_size,
-                                    const int32_t* ori_block_table, int32_t ori_table_len, const void* cmp_kv,
-                                    int64_t cmp_blocks, int32_t cmp_block_size, const int32_t* cmp_block_table,
-                                    int32_t cmp_table_len, const int32_t* cmp_sparse_indices, int32_t topk_cmp,
-                                    int32_t n_cmp, int32_t cmp_ratio, const float* sinks, float softmax_scale,
-                                    int32_t ori_win_left, void* out, float* lse, void* workspace,
-                                    size_t workspace_bytes, void* stream) {
+namespace {
+
+int flash_mla_entry(const void* q, int64_t T, int32_t N1, int32_t D, const int32_t* q_prefix,
+                    const int32_t* act_q_lens, const int32_t* seqused_kv, int64_t B, const void* ori_kv,
+                    int64_t ori_blocks, int32_t ori_block_size, const int32_t* ori_block_table, int32_t ori_table_len,
+                    const void* cmp_kv, int64_t cmp_blocks, int32_t cmp_block_size, const int32_t* cmp_block_table,
+                    int32_t cmp_table_len, const int32_t* cmp_sparse_indices, int32_t topk_cmp, int32_t n_cmp,
+                    int32_t cmp_ratio, const float* sinks, float softmax_scale, int32_t ori_win_left, void* out,
+                    float* lse, void* workspace, size_t workspace_bytes, void* stream, int32_t f16,
+                    const char* what) {
   using namespace dsa;
-  const char* what = "dsa_sparse_flash_mla";
   if (D != 512) return set_error(kUnsupported, "%s: only D = 512 is built (got %d)", what, D);
   if (T < 0 || B < 0 || N1 <= 0 || ori_win_left < 0 || n_cmp < 0)
     return set_error(kInvalidArgument, "%s: bad sizes", what);
@@ -109,5 +109,38 @@ extern "C" int dsa_sparse_flash_mla(const void* q, int64_t T, int32_t N1, int32_
   r.workspace = workspace;
   r.workspace_bytes = workspace_bytes;
   r.stream = stream;
+  r.f16 = f16;
   return sparse_mla_run(r, what);
+}
+
+}  // namespace
+
+extern "C" int dsa_sparse_flash_mla(const void* q, int64_t T, int32_t N1, int32_t D, const int32_t* q_prefix,
+                                    const int32_t* act_q_lens, const int32_t* seqused_kv, int64_t B,
+                                    const void* ori_kv, int64_t ori_blocks, int32_t ori_block_size,
+                                    const int32_t* ori_block_table, int32_t ori_table_len, const void* cmp_kv,
+                                    int64_t cmp_blocks, int32_t cmp_block_size, const int32_t* cmp_block_table,
+                                    int32_t cmp_table_len, const int32_t* cmp_sparse_indices, int32_t topk_cmp,
+                                    int32_t n_cmp, int32_t cmp_ratio, const float* sinks, float softmax_scale,
+                                    int32_t ori_win_left, void* out, float* lse, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  return flash_mla_entry(q, T, N1, D, q_prefix, act_q_lens, seqused_kv, B, ori_kv, ori_blocks, ori_block_size,
+                         ori_block_table, ori_table_len, cmp_kv, cmp_blocks, cmp_block_size, cmp_block_table,
+                         cmp_table_len, cmp_sparse_indices, topk_cmp, n_cmp, cmp_ratio, sinks, softmax_scale,
+                         ori_win_left, out, lse, workspace, workspace_bytes, stream, 0, "dsa_sparse_flash_mla");
+}
+
+extern "C" int dsa_sparse_flash_mla_f16(const void* q, int64_t T, int32_t N1, int32_t D, const int32_t* q_prefix,
+                                        const int32_t* act_q_lens, const int32_t* seqused_kv, int64_t B,
+                                        const void* ori_kv, int64_t ori_blocks, int32_t ori_block_size,
+                                        const int32_t* ori_block_table, int32_t ori_table_len, const void* cmp_kv,
+                                        int64_t cmp_blocks, int32_t cmp_block_size, const int32_t* cmp_block_table,
+                                        int32_t cmp_table_len, const int32_t* cmp_sparse_indices, int32_t topk_cmp,
+                                        int32_t n_cmp, int32_t cmp_ratio, const float* sinks, float softmax_scale,
+                                        int32_t ori_win_left, void* out, float* lse, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return flash_mla_entry(q, T, N1, D, q_prefix, act_q_lens, seqused_kv, B, ori_kv, ori_blocks, ori_block_size,
+                         ori_block_table, ori_table_len, cmp_kv, cmp_blocks, cmp_block_size, cmp_block_table,
+                         cmp_table_len, cmp_sparse_indices, topk_cmp, n_cmp, cmp_ratio, sinks, softmax_scale,
+                         ori_win_left, out, lse, workspace, workspace_bytes, stream, 1, "dsa_sparse_flash_mla_f16");
 }

@@ -87,6 +87,17 @@ using dsa::xor16_sum;
 using dsa::xor32_max;
 using dsa::xor32_sum;
 
+// 16x16x32 MFMA on 16-bit operands held as raw dwords (F16: IEEE half, else bf16).
+template <bool F16>
+__device__ __forceinline__ dsa::f32x4 mfma16x16x32(dsa::i32x4 a, dsa::i32x4 b, dsa::f32x4 c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(dsa::f16x8, a), __builtin_bit_cast(dsa::f16x8, b),
+                                                  c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dsa::bf16x8, a),
+                                                   __builtin_bit_cast(dsa::bf16x8, b), c, 0, 0, 0);
+}
+
 // Source of the gathers for invalid keys: always in bounds, always zero.
 __device__ __align__(16) uint16_t g_zero_row[576];
 
@@ -188,7 +199,7 @@ __device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, 
 // each) and one's prologue / epilogue runs beside the other's steps.  (WAVES = 8,
 // one 128-head workgroup per CU, measured slower than the 4-wave 128-head form
 // below and is not launched.)
-template <int DQK, int kStages, int WAVES>
+template <int DQK, int kStages, int WAVES, bool F16>
 __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaParams p) {
   constexpr int NT = WAVES * 64;
   constexpr int HPG = 16 * WAVES;  // heads per workgroup
@@ -239,15 +250,13 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
   // ---- Q^T operand: lane (g, c) holds head c, dims 64(ks/2) + 16g + 8(ks%2) .. +8,
   // i.e. 16-byte chunk 8(ks/2) + 2g + ks%2 (the chunk order the K reads use; any
   // order shared by both operands gives the same dot product)
-  dsa::bf16x8 qf[KSTEPS];
+  dsa::i32x4 qf[KSTEPS];
   {
     const uint16_t* qp = p.q + (token * p.H + (head_ok ? head : 0)) * DQK + 16 * g;
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-      dsa::i32x4 v = head_ok ? *reinterpret_cast<const dsa::i32x4*>(qp + 64 * (ks >> 1) + 8 * (ks & 1))
-                             : dsa::i32x4{0, 0, 0, 0};
-      qf[ks] = __builtin_bit_cast(dsa::bf16x8, v);
-    }
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      qf[ks] = head_ok ? *reinterpret_cast<const dsa::i32x4*>(qp + 64 * (ks >> 1) + 8 * (ks & 1))
+                       : dsa::i32x4{0, 0, 0, 0};
   }
 
   // ---- resolve this split's indices to physical rows (-1 = skip) ----
@@ -343,8 +352,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
         constexpr int fn = f + kPre;
         if constexpr (fn < 2 * KSTEPS)
           kfr[f % kPre] = lds_read_b128<(fn >> 2) * 4096 + (fn & 1) * 2048>((fn >> 1) & 1 ? kq1 : kq0);
-        acc[f & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dsa::bf16x8, cur), qf[f >> 1],
-                                                             acc[f & 1], 0, 0, 0);
+        acc[f & 1] = mfma16x16x32<F16>(cur, qf[f >> 1], acc[f & 1]);
         // keep the pipeline as written: fragment f + kPre's read, then MFMA f
         // (the compiler's own order measured ~2 % slower)
         __builtin_amdgcn_sched_barrier(0);
@@ -399,11 +407,10 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
         }
       // P^T operand: element 4kt + i = key 16kt + 4g + i
       dsa::i32x4 pb;
-      pb[0] = (int)dsa::pack_bf16x2(pr[0][0], pr[0][1]);
-      pb[1] = (int)dsa::pack_bf16x2(pr[0][2], pr[0][3]);
-      pb[2] = (int)dsa::pack_bf16x2(pr[1][0], pr[1][1]);
-      pb[3] = (int)dsa::pack_bf16x2(pr[1][2], pr[1][3]);
-      const dsa::bf16x8 pbf = __builtin_bit_cast(dsa::bf16x8, pb);
+      pb[0] = (int)dsa::pack_half2<F16>(pr[0][0], pr[0][1]);
+      pb[1] = (int)dsa::pack_half2<F16>(pr[0][2], pr[0][3]);
+      pb[2] = (int)dsa::pack_half2<F16>(pr[1][0], pr[1][1]);
+      pb[3] = (int)dsa::pack_half2<F16>(pr[1][2], pr[1][3]);
 
       // O^T[d, head] += V^T[d, keys] . P^T[keys, head].  The transposing load:
       // lane s of group g points at V[16r + 4g + s/4][16dt + 4(s%4)] (chunk
@@ -440,7 +447,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
           vfr[dt % kVPre][1] = lds_read_tr16<(dn >> 2) * 4096 + 2048>(vq[dn & 3]);
         }
         const dsa::i32x4 av = {v0[0], v0[1], v1[0], v1[1]};
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dsa::bf16x8, av), pbf, o[dt], 0, 0, 0);
+        o[dt] = mfma16x16x32<F16>(av, pb, o[dt]);
         __builtin_amdgcn_sched_barrier(0);
       });
     }
@@ -457,8 +464,8 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
 #pragma unroll
     for (int dt = 0; dt < kDV / 16; ++dt) {
       dsa::i32x2 v;
-      v[0] = (int)dsa::pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
-      v[1] = (int)dsa::pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
+      v[0] = (int)dsa::pack_half2<F16>(o[dt][0] * inv, o[dt][1] * inv);
+      v[1] = (int)dsa::pack_half2<F16>(o[dt][2] * inv, o[dt][3] * inv);
       *reinterpret_cast<dsa::i32x2*>(op + 16 * dt) = v;
     }
     if (g == 0 && p.lse) p.lse[token * p.H + head] = lse_v;
@@ -539,20 +546,31 @@ constexpr int kW4VPre = 4;    // P.V A fragments (two reads each) in flight
       DSA_A10(14), DSA_A10(15), DSA_A10(16), DSA_A10(17), DSA_A10(18), DSA_A10(19), DSA_A10(20), DSA_A10(21),        \
       DSA_A10(22), DSA_A10(23), DSA_A10(24), "a250", "a251", "a252", "a253", "a254", "a255"
 
-// S^T = K . Q^T (first k-step) and S^T += K . Q^T, in VGPRs
+// S^T = K . Q^T (first k-step) and S^T += K . Q^T, in VGPRs (F16: IEEE half
+// operands, else bf16)
+template <bool F16>
 __device__ __forceinline__ void mfma32_v0(f32x16& acc, dsa::i32x4 a, dsa::i32x4 b) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b) : DSA_AGPRS);
+  if constexpr (F16) asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b) : DSA_AGPRS);
+  else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b) : DSA_AGPRS);
 }
+template <bool F16>
 __device__ __forceinline__ void mfma32_v(f32x16& acc, dsa::i32x4 a, dsa::i32x4 b) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b) : DSA_AGPRS);
+  if constexpr (F16) asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b) : DSA_AGPRS);
+  else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b) : DSA_AGPRS);
 }
 // O^T d-tile DT += V^T . P^T
-template <int DT>
+template <int DT, bool F16>
 __device__ __forceinline__ void mfma32_o(dsa::i32x4 a, dsa::i32x4 b) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 a[%2:%3], %0, %1, a[%2:%3]"
-               :
-               : "v"(a), "v"(b), "i"(16 * DT), "i"(16 * DT + 15)
-               : DSA_AGPRS);
+  if constexpr (F16)
+    asm volatile("v_mfma_f32_32x32x16_f16 a[%2:%3], %0, %1, a[%2:%3]"
+                 :
+                 : "v"(a), "v"(b), "i"(16 * DT), "i"(16 * DT + 15)
+                 : DSA_AGPRS);
+  else
+    asm volatile("v_mfma_f32_32x32x16_bf16 a[%2:%3], %0, %1, a[%2:%3]"
+                 :
+                 : "v"(a), "v"(b), "i"(16 * DT), "i"(16 * DT + 15)
+                 : DSA_AGPRS);
 }
 // O^T = 0
 __device__ __forceinline__ void zero_o() {
@@ -649,7 +667,7 @@ __device__ __forceinline__ int32_t lds_read_b32(uint32_t addr) {
   return v;
 }
 
-template <int DQK>
+template <int DQK, bool F16>
 __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   constexpr int NT = 256;
   constexpr int KS = DQK / 16;          // score k-steps: 36 (576) or 32 (512)
@@ -813,8 +831,8 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
       const dsa::i32x4 cur = kfr[f % kW4KPre];
       constexpr int fn = f + kW4KPre;
       if constexpr (fn < KS) kfr[f % kW4KPre] = lds_read_b128<(fn / 4) * 4096>(sbase + kq[fn % 4]);
-      if constexpr (f == 0) mfma32_v0(acc, cur, qf[f]);
-      else mfma32_v(acc, cur, qf[f]);
+      if constexpr (f == 0) mfma32_v0<F16>(acc, cur, qf[f]);
+      else mfma32_v<F16>(acc, cur, qf[f]);
       if constexpr (vpf && f >= tail0 && f - tail0 < kW4VPre) v_read(vbase, IntC<f - tail0>{});
       hook(IntC<f>{});
       __builtin_amdgcn_sched_barrier(0);
@@ -877,7 +895,7 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
         l_run += sc[k - 1];
         pin(l_run);
         if constexpr ((k - 1) & 1) {
-          int w = (int)dsa::pack_bf16x2(sc[k - 2], sc[k - 1]);
+          int w = (int)dsa::pack_half2<F16>(sc[k - 2], sc[k - 1]);
           pin(w);
           pb[(k - 1) >> 3][((k - 1) & 7) >> 1] = w;
         }
@@ -923,7 +941,7 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
         vfr[f % kW4VPre][0] = lds_read_tr16<(dn >> 1) * 4096 + kn * 2048>(sbase + vq[dn & 1][0]);
         vfr[f % kW4VPre][1] = lds_read_tr16<(dn >> 1) * 4096 + kn * 2048>(sbase + vq[dn & 1][1]);
       }
-      mfma32_o<dt>(av, pp[kk]);
+      mfma32_o<dt, F16>(av, pp[kk]);
       hook(IntC<f>{});
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -1071,8 +1089,8 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         dsa::i32x2 v;
-        v[0] = (int)dsa::pack_bf16x2(t[4 * q4] * inv, t[4 * q4 + 1] * inv);
-        v[1] = (int)dsa::pack_bf16x2(t[4 * q4 + 2] * inv, t[4 * q4 + 3] * inv);
+        v[0] = (int)dsa::pack_half2<F16>(t[4 * q4] * inv, t[4 * q4 + 1] * inv);
+        v[1] = (int)dsa::pack_half2<F16>(t[4 * q4 + 2] * inv, t[4 * q4 + 3] * inv);
         o_put(4 * dt + q4, v);
       }
     });
@@ -1122,6 +1140,7 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
 constexpr int kCombineU = 8;
 constexpr int kCombineRows = 4;  // rows per 256-thread block
 
+template <bool F16>
 __global__ __launch_bounds__(256) void mla_combine_kernel(const uint16_t* __restrict__ part_o,
                                                           const float* __restrict__ part_lse,
                                                           const float* __restrict__ part_scale,
@@ -1174,15 +1193,15 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const uint16_t* __rest
   const float f = den > 0.f ? 1.f / den : 0.f;
   dsa::i32x4 ov;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) ov[e] = (int)dsa::pack_bf16x2(acc[2 * e] * f, acc[2 * e + 1] * f);
+  for (int e = 0; e < 4; ++e) ov[e] = (int)dsa::pack_half2<F16>(acc[2 * e] * f, acc[2 * e + 1] * f);
   *reinterpret_cast<dsa::i32x4*>(out + rh * kDV + 8 * d8) = ov;
   if (d8 == 0 && lse) lse[rh] = den > 0.f ? mx + __logf(den) : -__builtin_inff();
 }
 
-template <int DQK, int STAGES, int WAVES>
+template <int DQK, int STAGES, int WAVES, bool F16>
 int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   const size_t smem = (size_t)STAGES * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split;
-  auto fn = sparse_mla_kernel<DQK, STAGES, WAVES>;
+  auto fn = sparse_mla_kernel<DQK, STAGES, WAVES, F16>;
   static std::atomic<int> lds_reserved[dsa::kMaxDevices];
   const int rc = dsa::reserve_lds((const void*)fn, smem, lds_reserved, "sparse_mla");
   if (rc != dsa::kOk) return rc;
@@ -1190,10 +1209,10 @@ int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   return dsa::check_launch("dsa_sparse_mla_fwd");
 }
 
-template <int DQK>
+template <int DQK, bool F16>
 int launch_mla_w4(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   const size_t smem = (size_t)kW4Stages * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split;
-  auto fn = mla_w4_kernel<DQK>;
+  auto fn = mla_w4_kernel<DQK, F16>;
   static std::atomic<int> lds_reserved[dsa::kMaxDevices];
   const int rc = dsa::reserve_lds((const void*)fn, smem, lds_reserved, "sparse_mla");
   if (rc != dsa::kOk) return rc;
@@ -1206,11 +1225,11 @@ int launch_mla_w4(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
 // fewer heads: 4-wave, 64-head workgroups with 2-stage rings (<= 80 KB of LDS
 // each) that pair up on a CU, so one's prologue and epilogue runs beside the
 // other's steps -- when two of them fit in the CU's 160 KB of LDS.
-template <int DQK>
+template <int DQK, bool F16>
 int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   const size_t lds4 = (size_t)kStagesPair * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split + 64;
-  if (p.H <= 64 && 2 * lds4 <= 160 * 1024) return launch_mla_stages<DQK, kStagesPair, 4>(p, nblocks, stream);
-  return launch_mla_w4<DQK>(p, nblocks, stream);
+  if (p.H <= 64 && 2 * lds4 <= 160 * 1024) return launch_mla_stages<DQK, kStagesPair, 4, F16>(p, nblocks, stream);
+  return launch_mla_w4<DQK, F16>(p, nblocks, stream);
 }
 
 int choose_splits(int64_t tokens, int nhg, int topk) {
@@ -1309,11 +1328,17 @@ int sparse_mla_run(const MlaRun& r, const char* what) {
   const int64_t nblocks = ((units + kNumXcd - 1) / kNumXcd) * kNumXcd * p.nhg;
   if (nblocks > 0x7fffffff) return set_error(kUnsupported, "%s: grid too large", what);
   hipStream_t st = (hipStream_t)r.stream;
-  const int rc = r.d_qk == 576 ? launch_mla<576>(p, nblocks, st) : launch_mla<512>(p, nblocks, st);
+  const int rc = r.f16 ? (r.d_qk == 576 ? launch_mla<576, true>(p, nblocks, st) : launch_mla<512, true>(p, nblocks, st))
+                       : (r.d_qk == 576 ? launch_mla<576, false>(p, nblocks, st) : launch_mla<512, false>(p, nblocks, st));
   if (rc != kOk || ns == 1) return rc;
   const int64_t rows = T * r.H;
-  hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)((rows + kCombineRows - 1) / kCombineRows)), dim3(256), 0, st,
-                     p.part_o, p.part_lse, p.part_scale, rows, r.H, ns, p.out, r.lse);
+  const dim3 cgrid((unsigned)((rows + kCombineRows - 1) / kCombineRows));
+  if (r.f16)
+    hipLaunchKernelGGL(mla_combine_kernel<true>, cgrid, dim3(256), 0, st, p.part_o, p.part_lse, p.part_scale, rows, r.H,
+                       ns, p.out, r.lse);
+  else
+    hipLaunchKernelGGL(mla_combine_kernel<false>, cgrid, dim3(256), 0, st, p.part_o, p.part_lse, p.part_scale, rows,
+                       r.H, ns, p.out, r.lse);
   return check_launch("dsa_sparse_mla_fwd(combine)");
 }
 
@@ -1408,14 +1433,13 @@ extern "C" int dsa_sparse_mla_fwd_noalloc(const void* q, const void* kv, const i
   return dsa::sparse_mla_run(r, what);
 }
 
-extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices,
-                                  const int32_t* block_table, const int32_t* kv_len,
-                                  const int32_t* q_start, const float* attn_sink, int64_t B,
-                                  int64_t S, int32_t H, int32_t d_qk, int32_t d_v, int64_t skv,
-                                  int32_t block_size, int32_t max_blocks, int32_t topk,
-                                  float sm_scale, int32_t is_causal, int32_t num_splits, void* out,
-                                  float* lse, void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+namespace {
+
+int mla_fwd_entry(const void* q, const void* kv, const int32_t* indices, const int32_t* block_table,
+                  const int32_t* kv_len, const int32_t* q_start, const float* attn_sink, int64_t B, int64_t S,
+                  int32_t H, int32_t d_qk, int32_t d_v, int64_t skv, int32_t block_size, int32_t max_blocks,
+                  int32_t topk, float sm_scale, int32_t is_causal, int32_t num_splits, void* out, float* lse,
+                  void* workspace, size_t workspace_bytes, void* stream, int32_t f16, const char* what) {
   dsa::MlaRun r{};
   r.q = q;
   r.kv = kv;
@@ -1436,10 +1460,39 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
   r.sm_scale = sm_scale;
   r.is_causal = is_causal;
   r.num_splits = num_splits;
+  r.f16 = f16;
   r.out = out;
   r.lse = lse;
   r.workspace = workspace;
   r.workspace_bytes = workspace_bytes;
   r.stream = stream;
-  return dsa::sparse_mla_run(r, "dsa_sparse_mla_fwd");
+  return dsa::sparse_mla_run(r, what);
+}
+
+}  // namespace
+
+extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices,
+                                  const int32_t* block_table, const int32_t* kv_len,
+                                  const int32_t* q_start, const float* attn_sink, int64_t B,
+                                  int64_t S, int32_t H, int32_t d_qk, int32_t d_v, int64_t skv,
+                                  int32_t block_size, int32_t max_blocks, int32_t topk,
+                                  float sm_scale, int32_t is_causal, int32_t num_splits, void* out,
+                                  float* lse, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  return mla_fwd_entry(q, kv, indices, block_table, kv_len, q_start, attn_sink, B, S, H, d_qk, d_v, skv, block_size,
+                       max_blocks, topk, sm_scale, is_causal, num_splits, out, lse, workspace, workspace_bytes, stream,
+                       0, "dsa_sparse_mla_fwd");
+}
+
+extern "C" int dsa_sparse_mla_fwd_f16(const void* q, const void* kv, const int32_t* indices,
+                                      const int32_t* block_table, const int32_t* kv_len,
+                                      const int32_t* q_start, const float* attn_sink, int64_t B,
+                                      int64_t S, int32_t H, int32_t d_qk, int32_t d_v, int64_t skv,
+                                      int32_t block_size, int32_t max_blocks, int32_t topk,
+                                      float sm_scale, int32_t is_causal, int32_t num_splits, void* out,
+                                      float* lse, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  return mla_fwd_entry(q, kv, indices, block_table, kv_len, q_start, attn_sink, B, S, H, d_qk, d_v, skv, block_size,
+                       max_blocks, topk, sm_scale, is_causal, num_splits, out, lse, workspace, workspace_bytes, stream,
+                       1, "dsa_sparse_mla_fwd_f16");
 }

@@ -36,10 +36,16 @@ SIGNATURES = {
     "dsa_lightning_indexer_fp8_varlen": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32,
                                                  c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32,
                                                  c_i32, c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "dsa_lightning_indexer_h16_varlen": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32,
+                                                 c_i32, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32,
+                                                 c_i32, c_i32, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "dsa_sparse_mla_workspace_bytes": (c_sz, [c_i64, c_i64, c_i32, c_i32, c_i32]),
     "dsa_sparse_mla_fwd": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32,
                                    c_i32, c_i32, c_i64, c_i32, c_i32, c_i32, c_f32, c_i32, c_i32,
                                    c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "dsa_sparse_mla_fwd_f16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32,
+                                       c_i32, c_i32, c_i64, c_i32, c_i32, c_i32, c_f32, c_i32, c_i32,
+                                       c_vp, c_vp, c_vp, c_sz, c_vp]),
     "dsa_sparse_mla_fwd_noalloc": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32,
                                            c_i32, c_i32, c_i64, c_i32, c_i32, c_i32, c_f32, c_i32, c_i32,
                                            c_vp, c_vp, c_vp]),
@@ -47,12 +53,17 @@ SIGNATURES = {
     "dsa_sparse_flash_mla": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i32, c_vp,
                                      c_i32, c_vp, c_i64, c_i32, c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_f32,
                                      c_i32, c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "dsa_sparse_flash_mla_f16": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i32,
+                                         c_vp, c_i32, c_vp, c_i64, c_i32, c_vp, c_i32, c_vp, c_i32, c_i32, c_i32,
+                                         c_vp, c_f32, c_i32, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "dsa_block_sparse_indexer_logits": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32, c_i32, c_i32,
                                                 c_i64, c_i32, c_i32, c_i32, c_vp, c_vp]),
     "dsa_act_quant_int8": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_vp]),
     "dsa_quant_fp8_rows": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "dsa_indexer_k_append_fp8": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp]),
     "dsa_indexer_q_quant_fp8": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "dsa_quant_fp8_rows_f16": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
+    "dsa_indexer_q_quant_fp8_f16": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
 }
 
 _lock = threading.Lock()

@@ -149,9 +149,13 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
 
     Signature and validation of ``lightning_indexer``
     (examples/deepseek_v4/lightning_indexer.py:1202-1283); semantics of its golden
-    ``cpu_lightning_indexer`` (:199-335).  Differences: q/k are fp8 e4m3
-    (``torch.float8_e4m3fn``) with an optional per-key fp32 ``key_scale`` of shape
-    ``[B, S2]`` (or ``[B, S2, 1]``); returned ``values`` are fp32.  ``block_n``,
+    ``cpu_lightning_indexer`` (:199-335).  q/k are the reference's fp16 / bf16
+    (weights fp32 or q's dtype; a 16-bit MFMA kernel accumulating the exact
+    products in fp32, ``values`` in q's dtype as there), or fp8 e4m3
+    (``torch.float8_e4m3fn``, weights fp32, ``values`` fp32) for the fp8 MFMA
+    kernel.  Either takes an optional per-key fp32 ``key_scale`` of shape
+    ``[B, S2]`` (or ``[B, S2, 1]``) multiplying the logits.  N1 <= 64 (fewer heads
+    count as zero heads; the fp8 operands are padded to 64).  ``block_n``,
     ``pp_slots`` and ``max_cores`` were Ascend tiling knobs and are accepted and
     ignored.  Layouts (N2 = 1): query BSND ``[B, S1, N1, D]`` or TND ``[T, N1, D]``
     (``actual_seq_lengths_query`` = prefix sums); key BSND ``[B, S2, 1, D]``, TND
@@ -184,10 +188,11 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
         raise ValueError(f"next_tokens must be INT64_MAX, got {next_tokens}")
     if query.dtype != key.dtype:
         raise ValueError(f"query dtype {query.dtype} must equal key dtype {key.dtype}")
-    if query.dtype != _FP8:
-        raise ValueError(f"query/key dtype must be float8_e4m3fn, got {query.dtype}")
-    if weights.dtype != torch.float32:
-        raise ValueError(f"weights dtype {weights.dtype} must be float32")
+    half = query.dtype in (torch.float16, torch.bfloat16)
+    if not half and query.dtype != _FP8:
+        raise ValueError(f"query/key dtype must be float16 or bfloat16 (or float8_e4m3fn), got {query.dtype}")
+    if weights.dtype != torch.float32 and not (half and weights.dtype == query.dtype):
+        raise ValueError(f"weights dtype {weights.dtype} must be float32 or same as query {query.dtype}")
     is_tnd = layout_query == "TND"
     is_tnd_key = layout_key == "TND"
     if is_tnd and actual_seq_lengths_query is None:
@@ -284,8 +289,16 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
         raise AssertionError(f"N2 must be 1, got N2={N2}")
     if N1 > 64:
         raise ValueError(f"query head_num (N1) must be <= 64, got {N1}")
-    if N1 != 64:
-        raise NotImplementedError(f"the fp8 kernel is built for N1 = 64 index heads, got {N1}")
+    if half:
+        weights = weights.to(torch.float32).contiguous()
+    elif N1 != 64:
+        # the fp8 kernel holds 64 heads: zero heads (and zero weights) add nothing
+        pad_q = torch.zeros((*query.shape[:-2], 64, D), dtype=torch.uint8, device=dev)
+        pad_q[..., :N1, :] = query.view(torch.uint8)
+        query = pad_q.view(_FP8)
+        pad_w = torch.zeros((*weights.shape[:-1], 64), dtype=torch.float32, device=dev)
+        pad_w[..., :N1] = weights
+        weights, N1 = pad_w, 64
     ks = None
     if key_scale is not None:
         if key_scale.numel() != k_tokens:
@@ -298,13 +311,24 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
     L = lib()
     ws_bytes = L.dsa_lightning_indexer_varlen_workspace_bytes(q_tot, S2)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
-    check(L.dsa_lightning_indexer_fp8_varlen(_ptr(query), _ptr(key), _ptr(ks), _ptr(weights), _ptr(seq_q), seq_q_cum,
-                                             _ptr(seq_k), seq_k_cum, _ptr(bt), block_size, max_blocks, pool_rows,
-                                             B, S1, S2, q_tot, N1, D, sparse_count, sparse_mode, _ptr(indices),
-                                             _ptr(values), _ptr(ws), ws_bytes, _stream(dev)),
-          "dsa_lightning_indexer_fp8_varlen")
+    if half:
+        check(L.dsa_lightning_indexer_h16_varlen(_ptr(query), _ptr(key), _ptr(ks), _ptr(weights), _ptr(seq_q),
+                                                 seq_q_cum, _ptr(seq_k), seq_k_cum, _ptr(bt), block_size, max_blocks,
+                                                 pool_rows, B, S1, S2, q_tot, N1, D,
+                                                 int(query.dtype == torch.float16), sparse_count, sparse_mode,
+                                                 _ptr(indices), _ptr(values), _ptr(ws), ws_bytes, _stream(dev)),
+              "dsa_lightning_indexer_h16_varlen")
+    else:
+        check(L.dsa_lightning_indexer_fp8_varlen(_ptr(query), _ptr(key), _ptr(ks), _ptr(weights), _ptr(seq_q),
+                                                 seq_q_cum, _ptr(seq_k), seq_k_cum, _ptr(bt), block_size, max_blocks,
+                                                 pool_rows, B, S1, S2, q_tot, N1, D, sparse_count, sparse_mode,
+                                                 _ptr(indices), _ptr(values), _ptr(ws), ws_bytes, _stream(dev)),
+              "dsa_lightning_indexer_fp8_varlen")
+    out_dtype = query.dtype if half else torch.float32  # the golden's values are in q's dtype (:322)
     if values is None:
-        values = torch.empty((0,), dtype=torch.float32, device=dev)
+        values = torch.empty((0,), dtype=out_dtype, device=dev)
+    elif half:
+        values = values.to(out_dtype)
     if return_logits:
         logits = ws[: q_tot * S2 * 4].view(torch.float32).view(q_tot, S2)
         if not is_tnd:
@@ -351,8 +375,8 @@ def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor,
                    num_splits: int = 0, return_lse: bool = True):
     """Sparse MLA forward with one shared latent KV head -> ``(out, lse)``.
 
-    q ``[B, S, H, d_qk]`` bf16 (d_qk 576 = 512 latent + 64 rope, or 512);
-    kv ``[B, Skv, 1, d_qk]`` bf16, or a page pool ``[blocks, block_size, 1, d_qk]``
+    q ``[B, S, H, d_qk]`` bf16 or fp16 (d_qk 576 = 512 latent + 64 rope, or 512);
+    kv ``[B, Skv, 1, d_qk]`` of q's dtype, or a page pool ``[blocks, block_size, 1, d_qk]``
     with ``block_table [B, max_blocks]`` int32 (index i of batch b lives at
     ``pool[block_table[b, i // block_size], i % block_size]``,
     bench_sfa/sparse_flash_attn_pa_no_cv_pipeline.py:196-200); indices
@@ -362,12 +386,14 @@ def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor,
     ``-1`` and out-of-range indices are skipped; ``is_causal`` also skips indices
     above ``q_start_index_s + s`` (per batch if a tensor; default ``seq_len_kv[b] - S``,
     or ``Skv - S`` without ``seq_len_kv``, as example_sparse_flash_attn_mask_pa.py:221).
-    ``out [B, S, H, 512]`` bf16 and ``lse [B, S, H]`` fp32 (natural log,
+    ``out [B, S, H, 512]`` in q's dtype and ``lse [B, S, H]`` fp32 (natural log,
     sparse_flash_mla_golden.py:147-149).  A row without a valid index gets
-    out = 0 and lse = -inf.
+    out = 0 and lse = -inf.  fp16 runs fp16 MFMAs with the probabilities rounded
+    to fp16 before P.V (the reference's ``p.type(v.dtype)``,
+    example_sparse_flash_attn.py:288); bf16 rounds them to bf16.
     """
-    if q.dtype != torch.bfloat16 or kv.dtype != torch.bfloat16:
-        raise ValueError(f"q and kv must be bfloat16, got {q.dtype} and {kv.dtype}")
+    if q.dtype not in (torch.bfloat16, torch.float16) or kv.dtype != q.dtype:
+        raise ValueError(f"q and kv must both be bfloat16 or both float16, got {q.dtype} and {kv.dtype}")
     if indices.dtype != torch.int32:
         raise ValueError(f"indices must be int32, got {indices.dtype}")
     if q.dim() != 4 or kv.dim() != 4 or indices.dim() != 4:
@@ -413,15 +439,17 @@ def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor,
         sink = attn_sink.to(torch.float32).contiguous()
     if sm_scale is None:
         sm_scale = d_qk ** -0.5
-    out = torch.empty((B, S, H, d_v), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((B, S, H, d_v), dtype=q.dtype, device=dev)
     lse = torch.empty((B, S, H), dtype=torch.float32, device=dev)
     L = lib()
     ws_bytes = L.dsa_sparse_mla_workspace_bytes(B, S, H, topk, num_splits)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
-    check(L.dsa_sparse_mla_fwd(_ptr(q), _ptr(kv), _ptr(indices), _ptr(bt), _ptr(kvl), _ptr(qs), _ptr(sink),
-                               B, S, H, d_qk, d_v, skv, block_size, max_blocks, topk, float(sm_scale),
-                               int(bool(is_causal)), int(num_splits), _ptr(out), _ptr(lse), _ptr(ws),
-                               ws_bytes, _stream(dev)), "dsa_sparse_mla_fwd")
+    fn, name = ((L.dsa_sparse_mla_fwd_f16, "dsa_sparse_mla_fwd_f16") if q.dtype == torch.float16
+                else (L.dsa_sparse_mla_fwd, "dsa_sparse_mla_fwd"))
+    check(fn(_ptr(q), _ptr(kv), _ptr(indices), _ptr(bt), _ptr(kvl), _ptr(qs), _ptr(sink),
+             B, S, H, d_qk, d_v, skv, block_size, max_blocks, topk, float(sm_scale),
+             int(bool(is_causal)), int(num_splits), _ptr(out), _ptr(lse), _ptr(ws),
+             ws_bytes, _stream(dev)), name)
     return (out, lse) if return_lse else out
 
 
@@ -469,7 +497,7 @@ def sparse_attn_tilelang(query: torch.Tensor, key: torch.Tensor, value: torch.Te
     Row s attends to its indices ``<= actual_seq_lengths_kv[0] - actual_seq_lengths_query[0] + s``
     (the kernel's rule, :185, applied for sparse_mode 0 and 3 alike); rows
     ``s >= actual_seq_lengths_query[0]`` are not computed there and are zero here.
-    Returns ``[T, N, 512]`` bf16.  With rope parts the key cache is joined into one
+    Returns ``[T, N, 512]`` in query's dtype (bf16 or fp16).  With rope parts the key cache is joined into one
     ``[blocks, block_size, 1, 576]`` copy per call, as the reference does (:406);
     callers that keep a joined cache call ``sparse_mla_fwd`` on it directly."""
     if sparse_block_size != 1:
@@ -693,8 +721,8 @@ def sparse_flash_mla(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[
     assert ori_win_right == 0, "only ori_win_right=0 supported"
     assert layout_kv == "PA_ND", "only layout_kv=PA_ND supported"
     assert layout_q in ("TND", "BSND"), f"unsupported layout_q={layout_q!r}"
-    if q.dtype != torch.bfloat16:
-        raise ValueError(f"q must be bfloat16 (the built kernel), got {q.dtype}")
+    if q.dtype not in (torch.bfloat16, torch.float16):  # sparse_flash_mla_api.py:16-21
+        raise ValueError(f"unsupported torch dtype {q.dtype}")
     scenario = 1 if cmp_kv is None else (2 if cmp_sparse_indices is None else 3)
     # the small tensors (tables, lengths, sinks, lists) may live anywhere: they are
     # moved to q's device, as sparse_flash_mla_api.py:186-214 does
@@ -732,8 +760,8 @@ def sparse_flash_mla(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[
     if N1 != 64 or N2 != 1 or D != 512:
         raise ValueError(f"only N1=64, N2=1, D=512 supported (got N1={N1}, N2={N2}, D={D})")
     for name, t in (("q", q), ("ori_kv", ori_kv)) + ((("cmp_kv", cmp_kv),) if cmp_kv is not None else ()):
-        if t.dtype != torch.bfloat16:
-            raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+        if t.dtype != q.dtype:
+            raise ValueError(f"{name} must have q's dtype {q.dtype}, got {t.dtype}")
         _require_contiguous(name, t)
     ori_bt = ori_block_table.to(device=dev, dtype=torch.int32).contiguous()
     cmp_bt = cmp_block_table.to(device=dev, dtype=torch.int32).contiguous() if cmp_kv is not None else None
@@ -741,18 +769,19 @@ def sparse_flash_mla(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[
     qp = q_prefix.to(dev)
     kvl = seqused_kv.to(device=dev, dtype=torch.int32).contiguous()
     sk = sinks.to(device=dev, dtype=torch.float32).contiguous()
-    out = torch.empty((T, N1, D), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((T, N1, D), dtype=q.dtype, device=dev)
     lse = torch.empty((T, N1), dtype=torch.float32, device=dev)
     L = lib()
     wsb = L.dsa_sparse_flash_mla_workspace_bytes(T, N1, ori_win_left, n_cmp)
     ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
     cb, cbs, ctl = (cmp_kv.shape[0], cmp_kv.shape[1], cmp_bt.shape[1]) if cmp_kv is not None else (0, 0, 0)
-    check(L.dsa_sparse_flash_mla(_ptr(q), T, N1, D, _ptr(qp), _ptr(act_q), _ptr(kvl), B, _ptr(ori_kv),
-                                 ori_kv.shape[0], ori_kv.shape[1], _ptr(ori_bt), ori_bt.shape[1], _ptr(cmp_kv), cb,
-                                 cbs, _ptr(cmp_bt), ctl, _ptr(cmp_idx), K, n_cmp,
-                                 int(cmp_ratio) if cmp_ratio is not None else 0, _ptr(sk), float(softmax_scale),
-                                 ori_win_left, _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev)),
-          "dsa_sparse_flash_mla")
+    fn, name = ((L.dsa_sparse_flash_mla_f16, "dsa_sparse_flash_mla_f16") if q.dtype == torch.float16
+                else (L.dsa_sparse_flash_mla, "dsa_sparse_flash_mla"))
+    check(fn(_ptr(q), T, N1, D, _ptr(qp), _ptr(act_q), _ptr(kvl), B, _ptr(ori_kv),
+             ori_kv.shape[0], ori_kv.shape[1], _ptr(ori_bt), ori_bt.shape[1], _ptr(cmp_kv), cb,
+             cbs, _ptr(cmp_bt), ctl, _ptr(cmp_idx), K, n_cmp,
+             int(cmp_ratio) if cmp_ratio is not None else 0, _ptr(sk), float(softmax_scale),
+             ori_win_left, _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev)), name)
     if layout_q == "BSND":
         out = out.view(B, S_max, N1, D)
         lse = lse.view(B, S_max, N1)

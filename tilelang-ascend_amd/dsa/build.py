@@ -23,7 +23,8 @@ LIB_NAME = "libdsa_mi355x.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 ARCH = "gfx950"
 
-SOURCES = ["capi.cpp", "topk.hip", "indexer.hip", "sparse_mla.hip", "sparse_flash_mla.hip", "quant.hip", "block_sparse_indexer.hip"]
+SOURCES = ["capi.cpp", "topk.hip", "indexer.hip", "indexer_h16.hip", "sparse_mla.hip", "sparse_flash_mla.hip",
+           "quant.hip", "block_sparse_indexer.hip"]
 
 # Packed-fp32 VALU forms are disabled for all device code (they are generated
 # from ordinary float code at -O3 otherwise).
