@@ -152,6 +152,230 @@ def _time_launches(fn, steps: int, warmup: int = 2) -> float:
     return 1e3 * sum(a.elapsed_time(b) for a, b in evs) / steps
 
 
+DEC_BYTES = 64 * TOPK * (DQK * 2) + 64 * H * DQK * 2 + 64 * TOPK * 4 + 64 * 1024 * 4 + 64 * H * (DV * 2 + 4)
+
+
+def decode_config3(L, runs: int) -> dict:
+    """Config 3, sparse-MLA decode: B=64 single-token queries over 64K-token contexts
+    in 64-token pages of one 4.8 GB pool, top-2048 uniform indices; mean microseconds
+    per call (HIP events on the launch stream) over ``runs`` calls after 2 warm-ups."""
+    import torch
+
+    from dsa import inputs
+
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream(dev).cuda_stream
+    d = inputs.mla_decode(device=dev)
+    B = d["q"].shape[0]
+    out = torch.empty((B, 1, H, DV), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, 1, H), dtype=torch.float32, device=dev)
+    wsb = L.dsa_sparse_mla_workspace_bytes(B, 1, H, TOPK, 0)
+    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+    bt = d["block_table"]
+
+    def dec():
+        rc = L.dsa_sparse_mla_fwd(d["q"].data_ptr(), d["kv"].data_ptr(), d["indices"].data_ptr(), bt.data_ptr(),
+                                  d["seq_len_kv"].data_ptr(), None, None, B, 1, H, DQK, DV, d["kv"].shape[0] * 64,
+                                  64, bt.shape[1], TOPK, DQK ** -0.5, 0, 0, out.data_ptr(), lse.data_ptr(),
+                                  ws.data_ptr(), ws.numel(), st)
+        if rc != 0:
+            raise RuntimeError(f"decode: {L.dsa_last_error().decode()}")
+
+    us = _time_launches(dec, runs)
+    dec_bytes = B * TOPK * (DQK * 2) + B * H * DQK * 2 + B * TOPK * 4 + bt.numel() * 4 + B * H * (DV * 2 + 4)
+    assert dec_bytes == DEC_BYTES
+    return {"us": round(us, 2), "gbs": round(dec_bytes / us / 1e3, 1),
+            "frac_of_hbm": round(dec_bytes / us / 1e3 / PEAK_HBM_GBS, 4), "algorithmic_bytes": dec_bytes}
+
+
+def _profile_roles(dispatches):
+    """Label the DSA kernels of a --profile-run in dispatch order.  A layer step
+    launches indexer, topk, mla, dec_indexer, dec_topk, dec_mla in that order (a
+    combine after an MLA with split partials takes the MLA's role + "_combine");
+    an MLA launched where a layer step would start is a config-3 decode."""
+    seq = ("indexer", "topk", "mla", "dec_indexer", "dec_topk", "dec_mla")
+
+    def cat(name):
+        if "combine" in name:
+            return "comb"
+        if "indexer" in name:
+            return "idx"
+        if "topk" in name:
+            return "topk"
+        if "mla" in name:
+            return "mla"
+        return None
+
+    kind = {"indexer": "idx", "topk": "topk", "mla": "mla", "dec_indexer": "idx", "dec_topk": "topk",
+            "dec_mla": "mla"}
+    roles, prev, pos = [], None, 0
+    for name in dispatches:
+        c, role = cat(name), None
+        if c == "comb":
+            role = f"{prev}_combine" if prev and not prev.endswith("_combine") else None
+        elif c is not None:
+            if kind[seq[pos]] == c:
+                role = seq[pos]
+                pos = (pos + 1) % len(seq)
+            elif pos == 0 and c == "mla":
+                role = "config3_mla"
+        roles.append(role)
+        if role is not None:
+            prev = role
+    return roles
+
+
+PROFILE_PASSES = (("GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16",
+                   "SQ_INSTS_VALU_MFMA_MOPS_F8", "SQ_INSTS_VALU_MFMA_MOPS_F6F4", "SQ_INSTS_MFMA", "SQ_WAVES"),
+                  ("FETCH_SIZE",), ("WRITE_SIZE",))
+
+
+def summarize_profile(root: str) -> str:
+    """Text summary of the rocprofv3 runs of ``bench.py --profile-run`` under ``root``:
+    per DSA kernel role, the median over its dispatches of the kernel-trace duration,
+    the counters, the clock (GRBM_GUI_ACTIVE / 8 XCDs over the duration), the MFMA
+    busy fraction (SQ_VALU_MFMA_BUSY_CYCLES over 1024 SIMDs x those cycles) and the
+    HBM bytes (FETCH_SIZE and WRITE_SIZE in KiB, each scaled by what it reads for the
+    run's 1 GiB device copy)."""
+    import csv
+    import glob
+    import statistics
+
+    counters = {}  # run dir -> list of (dispatch id, kernel, {counter: value})
+    traces = []
+    for path in sorted(glob.glob(os.path.join(root, "**", "*counter_collection.csv"), recursive=True)):
+        per = {}
+        with open(path) as fh:
+            for r in csv.DictReader(fh):
+                key = int(r["Dispatch_Id"])
+                per.setdefault(key, [r["Kernel_Name"], {}])[1][r["Counter_Name"]] = float(r["Counter_Value"])
+        counters[path] = [(k, v[0], v[1]) for k, v in sorted(per.items())]
+    for path in sorted(glob.glob(os.path.join(root, "**", "*kernel_trace.csv"), recursive=True)):
+        with open(path) as fh:
+            traces = [(int(r["Dispatch_Id"]), r["Kernel_Name"], int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+                      for r in csv.DictReader(fh)]
+        traces.sort()
+
+    def by_role(rows, value):
+        out = {}
+        for role, row in zip(_profile_roles([r[1] for r in rows]), rows):
+            if role is not None:
+                out.setdefault(role, []).append(value(row))
+        return out
+
+    vals = {}
+    calib = {}
+    for rows in counters.values():
+        for _, name, c in rows:
+            if "copyBuffer" in name:
+                for cname in ("FETCH_SIZE", "WRITE_SIZE"):
+                    if cname in c and c[cname] > 100000:
+                        calib[cname] = 1073741824.0 / (c[cname] * 1024.0)
+        for role, lst in by_role(rows, lambda r: r[2]).items():
+            for c in lst:
+                for cname, v in c.items():
+                    vals.setdefault(role, {}).setdefault(cname, []).append(v)
+    dur = by_role(traces, lambda r: r[2] / 1000.0)
+    lines = [
+        "# rocprofv3 summary of bench.py --profile-run (1 GiB device copy, config 5 layer step x 13 = the bench's "
+        "3 warmup + 10 timed steps, config 3 decode x 3)",
+        "# made on one MI355X (repo root R, after cd /tmp && export TMPDIR=/tmp), one rocprofv3 run per line:",
+        f"#   rocprofv3 --pmc {' '.join(PROFILE_PASSES[0])} -d R/gpurun_out/prof/p1 -o run --output-format csv "
+        "-- python3 R/bench.py --profile-run",
+        "#   rocprofv3 --pmc FETCH_SIZE -d R/gpurun_out/prof/p2 ... (same)",
+        "#   rocprofv3 --pmc WRITE_SIZE -d R/gpurun_out/prof/p3 ... (same)",
+        "#   rocprofv3 --kernel-trace --stats -d R/gpurun_out/prof/kt -o run --output-format csv -- python3 "
+        "R/bench.py --profile-run",
+        "#   python3 R/bench.py --summarize-profile R/gpurun_out/prof",
+        f"# calibration (1 GiB device copy): FETCH_SIZE x {calib.get('FETCH_SIZE', float('nan')):.4f}, "
+        f"WRITE_SIZE x {calib.get('WRITE_SIZE', float('nan')):.4f} bytes per KiB read / 1024",
+        "# role: median over the role's dispatches (trace_mean/min/max_us: mean, min, max of its kernel-trace "
+        "durations); mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x "
+        "GRBM_GUI_ACTIVE / 8); clock_ghz = GRBM_GUI_ACTIVE / 8 / trace_us",
+    ]
+    for role in ("indexer", "topk", "mla", "mla_combine", "dec_indexer", "dec_topk", "dec_mla", "dec_mla_combine",
+                 "config3_mla", "config3_mla_combine"):
+        if role not in vals and role not in dur:
+            continue
+        m = {k: statistics.median(v) for k, v in vals.get(role, {}).items()}
+        t = statistics.median(dur[role]) if role in dur else None
+        out = {"trace_us": round(t, 2) if t else None}
+        if role in dur:
+            out["trace_mean_us"] = round(statistics.fmean(dur[role]), 2)
+            out["trace_min_us"] = round(min(dur[role]), 2)
+            out["trace_max_us"] = round(max(dur[role]), 2)
+        grbm = m.get("GRBM_GUI_ACTIVE")
+        if grbm and t:
+            out["clock_ghz"] = round(grbm / 8 / (t * 1e3), 3)
+        if grbm and "SQ_VALU_MFMA_BUSY_CYCLES" in m:
+            out["mfma_busy"] = round(m["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024 * grbm / 8), 4)
+        for cname, label in (("SQ_INSTS_VALU_MFMA_MOPS_BF16", "mfma_flops_bf16"),
+                             ("SQ_INSTS_VALU_MFMA_MOPS_F8", "mfma_flops_f8"),
+                             ("SQ_INSTS_VALU_MFMA_MOPS_F6F4", "mfma_flops_f6f4")):
+            if m.get(cname):
+                out[label] = float(f"{m[cname] * 512:.4e}")
+        if "FETCH_SIZE" in m and "FETCH_SIZE" in calib:
+            out["fetch_bytes"] = float(f"{m['FETCH_SIZE'] * 1024 * calib['FETCH_SIZE']:.4e}")
+        if "WRITE_SIZE" in m and "WRITE_SIZE" in calib:
+            out["write_bytes"] = float(f"{m['WRITE_SIZE'] * 1024 * calib['WRITE_SIZE']:.4e}")
+        if "fetch_bytes" in out and "write_bytes" in out:
+            out["hbm_bytes"] = float(f"{out['fetch_bytes'] + out['write_bytes']:.4e}")
+        for cname in ("SQ_INSTS_MFMA", "SQ_WAVES", "SQ_BUSY_CU_CYCLES", "GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES"):
+            if cname in m:
+                out[cname] = float(f"{m[cname]:.5e}")
+        lines.append(f"role={role} " + " ".join(f"{k}={v}" for k, v in out.items() if v is not None))
+    return "\n".join(lines)
+
+
+def summarize_trace(path: str, layer_steps: int) -> str:
+    """Per (phase, kernel, workgroups) durations from the rocprofv3 kernel trace
+    (``*kernel_trace.csv``) of a bench.py run: the first ``layer_steps`` x 7 DSA
+    dispatches are the layer steps (warmup and timed), the rest the target shapes;
+    torch, runtime-copy and BLAS helper kernels are left out."""
+    import csv
+    import glob
+
+    if os.path.isdir(path):
+        path = glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True)[0]
+    with open(path) as fh:
+        rows = [r for r in csv.DictReader(fh)
+                if not any(x in r["Kernel_Name"] for x in ("at::", "rocclr", "Cijk", "rocprim"))]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    agg = {}
+    for i, r in enumerate(rows):
+        name = r["Kernel_Name"].replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
+        grid = int(r.get("Grid_Size_X") or r.get("Grid_Size") or 0)
+        wg = int(r.get("Workgroup_Size_X") or r.get("Workgroup_Size") or 1)
+        phase = "layer" if i < 7 * layer_steps else "target"
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        agg.setdefault((phase, name, grid // max(wg, 1), wg), []).append((d, r))
+    lines = [f"{'phase':6s} {'kernel':36s} {'workgroups':>10s} {'wg_size':>7s} {'calls':>5s} {'avg_us':>9s} "
+             f"{'min_us':>9s} {'max_us':>9s} {'lds_B':>7s} {'vgpr':>5s} {'scratch':>7s}"]
+    for (ph, k, g, w), v in agg.items():
+        ds = [x[0] for x in v]
+        r0 = v[0][1]
+        vg = r0.get("VGPR_Count") or r0.get("Arch_VGPR_Count") or ""
+        lines.append(f"{ph:6s} {k[:36]:36s} {g:10d} {w:7d} {len(ds):5d} {sum(ds) / len(ds):9.2f} {min(ds):9.2f} "
+                     f"{max(ds):9.2f} {r0.get('LDS_Block_Size', ''):>7s} {vg:>5s} {r0.get('Scratch_Size', ''):>7s}")
+    return "\n".join(lines)
+
+
+def read_profile(path: str) -> dict:
+    """role -> {key: value} from a summarize_profile text (empty if missing)."""
+    out = {}
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if not line.startswith("role="):
+                    continue
+                kv = dict(tok.split("=", 1) for tok in line.split())
+                role = kv.pop("role")
+                out[role] = {k: float(v) for k, v in kv.items()}
+    except (OSError, ValueError):
+        return {}
+    return out
+
+
 def target_configs(L, steps: int) -> dict:
     """The single-kernel north-star shapes beside the layer step: sparse-MLA decode
     (B=64, 64K paged context) and prefill (Sq=Skv=16384), and indexer + top-k at
@@ -169,26 +393,7 @@ def target_configs(L, steps: int) -> dict:
             raise RuntimeError(f"{what}: {L.dsa_last_error().decode()}")
 
     # config 3: decode, B=64, 64K context in 64-token pages, top-2048
-    d = inputs.mla_decode(device=dev)
-    B = d["q"].shape[0]
-    out = torch.empty((B, 1, H, DV), dtype=torch.bfloat16, device=dev)
-    lse = torch.empty((B, 1, H), dtype=torch.float32, device=dev)
-    wsb = L.dsa_sparse_mla_workspace_bytes(B, 1, H, TOPK, 0)
-    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
-    bt = d["block_table"]
-
-    def dec():
-        chk(L.dsa_sparse_mla_fwd(d["q"].data_ptr(), d["kv"].data_ptr(), d["indices"].data_ptr(), bt.data_ptr(),
-                                 d["seq_len_kv"].data_ptr(), None, None, B, 1, H, DQK, DV, d["kv"].shape[0] * 64,
-                                 64, bt.shape[1], TOPK, DQK ** -0.5, 0, 0, out.data_ptr(), lse.data_ptr(),
-                                 ws.data_ptr(), ws.numel(), st), "decode")
-
-    us = _time_launches(dec, steps)
-    dec_bytes = B * TOPK * (DQK * 2) + B * H * DQK * 2 + B * TOPK * 4 + bt.numel() * 4 + B * H * (DV * 2 + 4)
-    res["decode_b64_64k"] = {"us": round(us, 2), "gbs": round(dec_bytes / us / 1e3, 1),
-                             "frac_of_hbm": round(dec_bytes / us / 1e3 / PEAK_HBM_GBS, 4),
-                             "algorithmic_bytes": dec_bytes}
-    del d, out, lse, ws, bt
+    res["decode_b64_64k"] = decode_config3(L, runs=steps)
     torch.cuda.empty_cache()
 
     # config 4: prefill, Sq = Skv = 16384, causal index ranges, top-2048
@@ -394,13 +599,98 @@ def flash_mla_v4_configs(L, steps: int) -> dict:
     return res
 
 
-def cpu_baseline(S1: int, S2: int, budget_rows: int = 2048, mla_tokens: int = 4096) -> dict:
-    """Time the CPU oracle on a bounded sample of the same workload and scale it."""
+def _median_time(fn, runs: int = 3, warmup: int = 1) -> float:
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_baseline_configs() -> dict:
+    """The oracle (torch on the host cores) on configs 1-4 of the baseline: 1 warm-up
+    + median of 3 for configs 1-3, one run of a stated subsample for config 4.
+    Inputs are the configs' own generators (dsa.inputs, seeded) on the CPU."""
     import torch
 
     from dsa import inputs
     from oracle.dsa_oracle import indexer_scores, sparse_mla_fwd_gather, stable_topk
 
+    res = {}
+    # config 1: sparse MLA, B=1 S=128 Skv=4096 H=16 topk=512 (the whole config)
+    c1 = inputs.mla_prefill()
+    f1 = lambda: sparse_mla_fwd_gather(c1["q"], c1["kv"], c1["indices"], c1["sm_scale"],  # noqa: E731
+                                       q_start_index_s=c1["q_start"], is_causal=True, p_dtype=torch.bfloat16)
+    t = _median_time(f1)
+    fl = 2.0 * 16 * 512 * 1088 * 128
+    res["config1_mla_small"] = {"s": round(t, 4), "tflops": round(fl / t / 1e12, 4), "sample": "whole config"}
+    del c1
+    # config 2: indexer + top-k, 4096 x 32768, causal, K = 2048: the last 256 query
+    # rows (the config's inputs, seed 2), scaled to the 4096 rows by the visible
+    # (query, key) pairs
+    S1c, S2c, nr = 4096, 32768, 256
+    ix = inputs.indexer_fp8(B=1, S1=S1c, S2=S2c, seed=2)
+    k = ix["k"][0, :, 0].float() * ix["key_scale"][0].unsqueeze(1)
+    qf, w = ix["q"][0, S1c - nr:].float().contiguous(), ix["w"][0, S1c - nr:].contiguous()
+    vis = torch.arange(S2c - nr + 1, S2c + 1)  # causal lengths of the sample rows
+
+    def f2():
+        sc = indexer_scores(qf, k, w, nr, S2c, 0)
+        sc.masked_fill_(torch.arange(S2c)[None, :] >= vis[:, None], float("-inf"))
+        stable_topk(sc, 2048, row_len=vis)
+
+    t = _median_time(f2)
+    pairs_all = sum(S2c - S1c + r + 1 for r in range(S1c))
+    scaled = t * pairs_all / int(vis.sum())
+    res["config2_indexer_topk_32k"] = {"s_sample": round(t, 3), "us_scaled": round(scaled * 1e6, 1),
+                                       "sample": f"last {nr} of {S1c} query rows, scaled by visible pairs"}
+    del ix, k, qf, w
+    # config 3: decode B=64, H=128, topk=2048 over 64K paged contexts.  The oracle's
+    # work is the gather of 64 x 2048 pool rows and the attention over them; the
+    # pool here holds 4096 pages of 64 rows (302 MB) instead of 65536, so that the
+    # baseline does not spend a minute generating 4.8 GB: the same rows are
+    # gathered, from a smaller pool
+    c3 = inputs.mla_decode(B=64, ctx=65536, pool_blocks=4096, seed=3)
+    f3 = lambda: sparse_mla_fwd_gather(c3["q"], c3["kv"], c3["indices"], c3["sm_scale"],  # noqa: E731
+                                       block_table=c3["block_table"], is_causal=False, p_dtype=torch.bfloat16)
+    t = _median_time(f3)
+    res["config3_decode_b64_64k"] = {"s": round(t, 4), "us": round(t * 1e6, 1),
+                                     "sample": "whole batch; 4096-page pool (same gathers)"}
+    del c3
+    # config 4: prefill Sq = Skv = 16384, causal, topk 2048: one run over the last
+    # 512 query rows (each with 2048 valid indices), scaled to the 16384 rows by
+    # their valid-index counts
+    # (inputs of the config's distribution drawn for the sample rows only: q and kv
+    # N(0, 1) * 0.5 in bf16, row i's indices the first 2048 of a random order of [0, i])
+    S, nr = 16384, 512
+    g = torch.Generator().manual_seed(4)
+    q4 = (torch.randn((1, nr, 128, 576), generator=g) * 0.5).to(torch.bfloat16)
+    kv4 = (torch.randn((1, S, 1, 576), generator=g) * 0.5).to(torch.bfloat16)
+    idx4 = torch.stack([torch.randperm(i + 1, generator=g)[:2048] for i in range(S - nr, S)]).int()
+    t0 = time.perf_counter()
+    sparse_mla_fwd_gather(q4, kv4, idx4.view(1, nr, 1, 2048), 576 ** -0.5, q_start_index_s=S - nr,
+                          is_causal=True, p_dtype=torch.bfloat16)
+    t = time.perf_counter() - t0
+    valid_all = sum(min(i + 1, 2048) for i in range(S))
+    scaled = t * valid_all / (nr * 2048)
+    res["config4_prefill_16k"] = {"s_sample": round(t, 3), "s_scaled": round(scaled, 2),
+                                  "tflops": round(2.0 * 128 * 2048 * 1088 * S / scaled / 1e12, 4),
+                                  "sample": f"last {nr} of {S} rows, one run, scaled by valid indices"}
+    return res
+
+
+def cpu_baseline(S1: int, S2: int, budget_rows: int = 2048, mla_tokens: int = 4096) -> dict:
+    """Time the CPU oracle on a bounded sample of the same workload and scale it,
+    plus configs 1-4 (cpu_baseline_configs); all host cores."""
+    import torch
+
+    from dsa import inputs
+    from oracle.dsa_oracle import indexer_scores, sparse_mla_fwd_gather, stable_topk
+
+    torch.set_num_threads(os.cpu_count() or 1)
     threads = torch.get_num_threads()
     ix = inputs.indexer_fp8(B=1, S1=budget_rows, S2=S2, seed=5)
     k = ix["k"][0, :, 0].float() * ix["key_scale"][0].unsqueeze(1)
@@ -418,6 +708,7 @@ def cpu_baseline(S1: int, S2: int, budget_rows: int = 2048, mla_tokens: int = 40
     sparse_mla_fwd_gather(q, kv, idx.view(1, mla_tokens, 1, TOPK), None, is_causal=False,
                           p_dtype=torch.bfloat16)
     t4 = time.perf_counter()
+    del ix, k, sc, q, kv, idx
     scale_rows = S1 / budget_rows
     return {
         "value": mla_flops(mla_tokens) / (t4 - t3) / 1e12,
@@ -428,8 +719,10 @@ def cpu_baseline(S1: int, S2: int, budget_rows: int = 2048, mla_tokens: int = 40
                    f"sparse MLA on {mla_tokens} of {S1} tokens; value = MLA TFLOP/s on the sample"),
         "indexer_topk_us_scaled": (t2 - t0) * scale_rows * 1e6,
         "mla_us_scaled": (t4 - t3) * (S1 / mla_tokens) * 1e6,
+        "configs": cpu_baseline_configs(),
         "cpu_model": _cpu_model(),
         "os_cpu_count": os.cpu_count(),
+        "torch_threads": threads,
     }
 
 
@@ -455,12 +748,25 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-targets", action="store_true",
                     help="skip the single-kernel decode / prefill / 32K indexer timings")
-    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_indexer_layer128k.txt"),
-                    help="rocprofv3 --pmc summary holding the dominant kernel's HBM bytes per launch")
-    ap.add_argument("--traffic-run", action="store_true",
-                    help="for rocprofv3 --pmc: one 1 GiB device copy (counter calibration), then one "
-                         "layer step; prints no benchmark line")
+    ap.add_argument("--profile", default=os.path.join(ROOT, "profiles", "pmc_dsa_layer128k.txt"),
+                    help="rocprofv3 summary written by --summarize-profile (counters of the layer's kernels)")
+    ap.add_argument("--profile-run", action="store_true",
+                    help="for rocprofv3 (one --pmc pass or --kernel-trace per run): one 1 GiB device copy "
+                         "(counter calibration), two warm-up layer steps, one layer step and one config-3 "
+                         "decode (B=64, 64K paged); prints no benchmark line")
+    ap.add_argument("--summarize-trace", metavar="PATH",
+                    help="per-kernel durations from the rocprofv3 --kernel-trace output (a directory or its "
+                         "*kernel_trace.csv) of a bench.py run with the same --steps / --warmup")
+    ap.add_argument("--summarize-profile", metavar="DIR",
+                    help="summarise the rocprofv3 runs of --profile-run under DIR (subdirectories holding "
+                         "*counter_collection.csv or *kernel_trace.csv) and print the profile text")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace, args.warmup + args.steps))
+        return 0
+    if args.summarize_profile:
+        print(summarize_profile(args.summarize_profile))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this path "
               "(each GPU box has one GPU)", file=sys.stderr)
@@ -469,14 +775,22 @@ def main() -> int:
 
     layer = Layer(args.s1, args.s2, args.dec_batch)
     torch.cuda.synchronize()
-    if args.traffic_run:
+    if args.profile_run:
         src = torch.ones((1 << 28,), dtype=torch.float32, device="cuda:0")  # 1 GiB
         dst = torch.empty_like(src)
         dst.copy_(src)
+        del src, dst
         torch.cuda.synchronize()
-        layer.step()
+        for _ in range(args.warmup + args.steps):
+            layer.step()
         torch.cuda.synchronize()
-        print("traffic run: copy of 1073741824 bytes, then one layer step", flush=True)
+        lib_handle = layer.L
+        del layer
+        torch.cuda.empty_cache()
+        decode_config3(lib_handle, runs=3)
+        torch.cuda.synchronize()
+        print(f"profile run: copy of 1073741824 bytes, {args.warmup + args.steps} layer steps, three config-3 "
+              "decodes", flush=True)
         return 0
     for _ in range(args.warmup):
         layer.step()
@@ -507,15 +821,8 @@ def main() -> int:
             "topk": ("hbm", topk_gbs, PEAK_HBM_GBS, "GB/s")}
     dom = max(kern, key=lambda k: per[k])
     bound, ach, peak, unit = kern[dom]
-    traffic = None
-    if os.path.exists(args.traffic):
-        try:
-            with open(args.traffic) as f:
-                for line in f:
-                    if line.startswith("hbm_bytes_per_launch"):
-                        traffic = float(line.split("=", 1)[1])
-        except (OSError, ValueError):
-            traffic = None
+    prof = read_profile(args.profile).get(dom, {})
+    traffic = prof.get("hbm_bytes")
     res = {
         "metric": METRIC,
         "value": round(mla_tflops, 2),
@@ -544,7 +851,14 @@ def main() -> int:
         "decode_us": {"indexer": round(per["dec_indexer"], 2), "topk": round(per["dec_topk"], 2),
                       "mla": round(per["dec_mla"], 2)},
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
-                     "frac": round(ach / peak, 4), "traffic": traffic},
+                     "frac": round(ach / peak, 4), "traffic": traffic,
+                     "traffic_source": (f"{os.path.relpath(args.profile, ROOT)} (rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                                        f"of bench.py --profile-run, copy-calibrated)") if traffic else None,
+                     "event_us": round(per[dom], 2), "profiled_us": prof.get("trace_us"),
+                     "profiled_frac": (round(ach * per[dom] / prof["trace_us"] / peak, 4)
+                                       if prof.get("trace_us") else None),
+                     "profiled_mfma_flops": prof.get("mfma_flops_f8") or prof.get("mfma_flops_bf16"),
+                     "profiled_mfma_busy": prof.get("mfma_busy"), "profiled_clock_ghz": prof.get("clock_ghz")},
     }
     if not args.no_targets:
         lib_handle = layer.L
