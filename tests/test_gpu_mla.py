@@ -8,7 +8,7 @@ import torch
 
 import dsa
 from dsa import inputs
-from oracle.dsa_oracle import sparse_mla_fwd_gather
+from oracle.dsa_oracle import sparse_mla_fwd_dense, sparse_mla_fwd_gather
 
 pytestmark = pytest.mark.gpu
 
@@ -95,6 +95,29 @@ def test_reference_factory_fp16_sentinel_convention(gpu):
     out = kern(inp["q"].to(gpu), inp["kv"].to(gpu), idx.to(gpu)).float().cpu()
     ro, _ = sparse_mla_fwd_gather(inp["q"], inp["kv"], inp["indices"], None, q_start_index_s=900,
                                   is_causal=True, p_dtype=torch.bfloat16)
+    torch.testing.assert_close(out, ro, **OUT_TOL)
+
+
+@pytest.mark.parametrize("S,sk,kv_stride,topk", [(64, 512, 4, 128), (16, 4, 4, 64), (40, 96, 2, 64)])
+def test_reference_factory_kv_stride(gpu, S, sk, kv_stride, topk):
+    # compressed KV rows (kv_stride > 1): the golden's causal rule over compressed
+    # positions, q_start = sk * kv_stride - S, and key 0 kept for the first
+    # kv_stride - 1 rows (example_sparse_flash_attn.py:255-292); every list holds
+    # key 0 and future keys, padded with the sentinel sk
+    g = torch.Generator().manual_seed(100 + S + kv_stride)
+    q = torch.randn((1, S, 128, 576), generator=g).to(torch.bfloat16)
+    kv = torch.randn((1, sk, 1, 576), generator=g).to(torch.bfloat16)
+    idx = torch.full((1, S, 1, topk), sk, dtype=torch.int32)
+    n = min(topk, sk)
+    for t in range(S):
+        perm = torch.randperm(sk, generator=g)[:n]
+        if not (perm == 0).any():
+            perm[0] = 0
+        idx[0, t, 0, :n] = perm.to(torch.int32)
+    print(f"factory kv_stride={kv_stride} S={S} sk={sk}", flush=True)
+    kern = dsa.sparse_attention_fwd(heads=128, dim=512, tail_dim=64, topk=topk, kv_stride=kv_stride)
+    out = kern(q.to(gpu), kv.to(gpu), idx.to(gpu)).float().cpu()
+    ro, _ = sparse_mla_fwd_dense(q, kv, idx, kv_stride=kv_stride, sm_scale=576 ** -0.5)
     torch.testing.assert_close(out, ro, **OUT_TOL)
 
 

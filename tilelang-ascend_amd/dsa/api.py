@@ -459,7 +459,16 @@ def sparse_attention_fwd(heads: int, dim: int, tail_dim: int, topk: int, kv_stri
     """Factory with the signature of the reference's ``sparse_attention_fwd``
     (examples/sparse_flash_attention/example_sparse_flash_attn.py:18-46), returning
     ``kernel(q, kv, indices) -> out``.  Asserts as the reference does; the
-    out-of-range sentinel ``Skv`` used to pad its indices (:303) is skipped."""
+    out-of-range sentinel ``Skv`` used to pad its indices (:303) is skipped.
+
+    With ``kv_stride > 1`` the KV rows are compressed positions: row n stands for
+    original keys up to ``n * kv_stride + kv_stride - 1`` and query m (at original
+    position ``Skv * kv_stride - S + m``) sees it when that position is at least
+    ``n * kv_stride + kv_stride - 1``, the causal rule of the golden
+    ``ref_sparse_attention_fwd_interface`` (:255-280); its first ``kv_stride - 1``
+    rows also keep a listed key 0 (:280; a row whose list lacks key 0 is not
+    given one).  Indices that fail the rule are set to -1 on the device before
+    the launch."""
     def _pow2(x):
         return x > 0 and (x & (x - 1)) == 0
     assert _pow2(dim), f"haven't check padding correctness yet, dim={dim}"
@@ -468,14 +477,21 @@ def sparse_attention_fwd(heads: int, dim: int, tail_dim: int, topk: int, kv_stri
     assert topk % block_I == 0, "otherwise will load some index=0 thus causing wrong kv to be loaded"
     if kv_group != 1:
         raise NotImplementedError("one latent KV head (kv_group = 1) only")
-    if kv_stride != 1:
-        raise NotImplementedError("kv_stride = 1 only")
+    if kv_stride < 1:
+        raise ValueError(f"kv_stride must be >= 1, got {kv_stride}")
     scale = (1.0 / (dim + tail_dim)) ** 0.5 if sm_scale is None else sm_scale
 
     def kernel(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         if q.shape[2] != heads or q.shape[3] != dim + tail_dim or indices.shape[3] != topk:
             raise ValueError("q / indices shape does not match the kernel's heads, dim + tail_dim, topk")
-        return sparse_mla_fwd(q, kv, indices, scale, is_causal=is_causal, return_lse=False)
+        if kv_stride == 1:
+            return sparse_mla_fwd(q, kv, indices, scale, is_causal=is_causal, return_lse=False)
+        S, skv = q.shape[1], kv.shape[1]
+        m = torch.arange(S, device=indices.device, dtype=torch.int64)
+        last = torch.div(skv * kv_stride - S + m + 1, kv_stride, rounding_mode="floor") - 1
+        last = torch.where(m < kv_stride - 1, last.clamp_min(0), last).view(1, S, 1, 1)
+        idx = torch.where(indices.to(torch.int64) <= last, indices, torch.full_like(indices, -1)).to(torch.int32)
+        return sparse_mla_fwd(q, kv, idx.contiguous(), scale, is_causal=False, return_lse=False)
 
     return kernel
 
