@@ -72,6 +72,29 @@ def test_d512_with_sink(gpu):
     _check(inp, gpu, attn_sink=sink, is_causal=False)
 
 
+@pytest.mark.parametrize("sink_value,splits,rising", [(-30.0, 1, True), (-30.0, 2, True), (2.0, 1, True),
+                                                      (None, 1, True), (-30.0, 1, False), (-30.0, 2, False)])
+def test_128_heads_rising_scores_with_sink(gpu, sink_value, splits, rising):
+    # 128 heads (the 4-wave form) with scores that grow (or shrink) along the index
+    # list, so that the reference maximum is raised in the first step (a sink far
+    # below the scores) and, rising, again in later steps, with O rescaled behind
+    # the P.V in flight; shrinking, the first step carries most of the weight and
+    # no later step raises the reference
+    inp = inputs.mla_prefill(B=1, S=4, Skv=4096, H=128, topk=2048, seed=21)
+    g = torch.Generator().manual_seed(2)
+    # the ramp scales the 64 rope dims only (scores move, values keep their size)
+    pos = torch.arange(4096, dtype=torch.float32) / 4096
+    ramp = 1.0 + 40.0 * (pos if rising else 1.0 - pos)
+    kv = inp["kv"].float()
+    kv[..., 512:] *= ramp.view(1, -1, 1, 1)
+    inp["kv"] = kv.to(torch.bfloat16)
+    inp["indices"] = torch.sort(inp["indices"], dim=-1)[0]
+    kw = dict(is_causal=True, num_splits=splits)
+    if sink_value is not None:
+        kw["attn_sink"] = torch.full((128,), sink_value) + 0.1 * torch.randn(128, generator=g)
+    _check(inp, gpu, **kw)
+
+
 def test_head_count_not_multiple_of_16(gpu):
     inp = inputs.mla_prefill(B=1, S=4, Skv=300, H=20, topk=96, seed=16)
     _check(inp, gpu)

@@ -71,6 +71,7 @@ struct MlaParams {
   int B, S, H, topk;
   int block_size, max_blocks;
   int nsplit, keys_per_split, nhg;
+  uint32_t buf_records;         // 16-byte records of the KV pool (buffer-addressed gathers of the 4-wave form)
   float scale_log2;
   int causal;
 };
@@ -641,22 +642,28 @@ __device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n s_nop 7\n
 // VALU write -> MFMA source read.
 __device__ __forceinline__ void valu_to_mfma() { asm volatile("s_nop 3" ::: "memory"); }
 
-// Ring layout of the 4-wave form.  A stage holds 32 keys x d_qk in 1 KB blocks
-// (key group kg = key / 8, chunk group cg = chunk / 8) at (cg * 4 + kg) * 1024.
-// Inside a block, chunk pair cp = (chunk % 8) / 2 owns 256 bytes holding the 8
-// keys' 32-byte pieces of that pair, key k at position k ^ 4 (cp % 2), and the
-// two 16-byte chunks of a piece swapped when kg is odd:
-//   offset = cp * 256 + (k ^ 4 (cp % 2)) * 32 + 16 ((chunk % 2) ^ (kg % 2)).
-// Then (a) one global_load_lds of 64 lanes still fetches 8 whole 128-byte rows,
-// (b) the score A fragments (one chunk of 16 keys per 16-lane group) hit 16
-// distinct 16-byte bank groups, and (c) every 16-lane group of a transposing P.V
-// read takes one contiguous 128-byte tile (4 keys x 16 dims), the dense pattern
-// that ds_read_b64_tr_b16 serves near its peak rate (about 2.8x the rate measured
-// for 4 rows at a 128-byte stride), with the two groups read together in
-// disjoint bank halves.
-__device__ __forceinline__ uint32_t w4_pos(int k, int cc, int kg) {
-  const int cp = cc >> 1;
-  return (uint32_t)(cp * 256 + ((k ^ (4 * (cp & 1))) * 32) + 16 * ((cc & 1) ^ (kg & 1)));
+// Ring layout of the 4-wave form.  A stage holds 32 keys x d_qk as one 1 KB block
+// per chunk pair cp (16-byte chunks 2 cp and 2 cp + 1, i.e. dims 16 cp .. 16 cp + 15)
+// at cp * 1024.  Key k's 32-byte piece sits at position k ^ 4 (cp % 2), its two
+// chunks swapped when k / 8 is odd:
+//   offset = cp * 1024 + (k ^ 4 (cp % 2)) * 32 + 16 ((chunk % 2) ^ (k / 8 % 2)).
+// Then (a) one 64-lane load fills one block (lane l: 16-byte slot l), (b) the score
+// A fragments (chunk pair ks, one 16-lane group per 16 keys) hit 16 distinct 16-byte
+// bank groups, and (c) every 16-lane group of a transposing P.V read takes one
+// contiguous 128-byte tile (4 keys x 16 dims), the dense pattern ds_read_b64_tr_b16
+// serves near its peak rate (about 2.8x the rate measured for 4 rows at a 128-byte
+// stride), the two groups read together falling in disjoint bank halves.
+__device__ __forceinline__ uint32_t w4_pos(int k, int cp, int c1) {
+  return (uint32_t)(cp * 1024 + ((k ^ (4 * (cp & 1))) * 32) + 16 * (c1 ^ ((k >> 3) & 1)));
+}
+
+// 16-byte LDS-direct load of record `idx` of a buffer of 16-byte records (zeros
+// past the buffer's end); OFF applies to both the global and the LDS address,
+// soff to the global address only.
+template <int OFF>
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, DSA_LDS void* lds, uint32_t idx,
+                                                  uint32_t soff) {
+  __builtin_amdgcn_struct_ptr_buffer_load_lds(rsrc, lds, 16, idx, 0, soff, OFF, 0);
 }
 
 // One 32-bit LDS read issued as inline asm (it joins the counted stream of the
@@ -667,7 +674,11 @@ __device__ __forceinline__ int32_t lds_read_b32(uint32_t addr) {
   return v;
 }
 
-template <int DQK, bool F16>
+// BUF: the gathers address the KV pool as a buffer of 16-byte records (a 32-bit
+// record index per lane; an index past the pool reads zeros), which issues in about
+// a fifth of the time of a 64-bit per-lane address.  The hardware forms the byte
+// offset in 32 bits, so this is for pools of at most 4 GiB with rows from one pool.
+template <int DQK, bool F16, bool BUF>
 __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   constexpr int NT = 256;
   constexpr int KS = DQK / 16;          // score k-steps: 36 (576) or 32 (512)
@@ -720,39 +731,46 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // rows[] written
   __builtin_amdgcn_s_barrier();                        // ... by every wave
 
-  // ---- gathers: wave w fills key group w (keys 8w .. 8w + 7 of the step) in
-  // every chunk group; 16-byte lane l of a block load writes byte 16 l of the
-  // block, i.e. chunk pair l / 16, key ((l / 2) % 8) ^ 4 (l / 16 % 2), chunk of
-  // the pair (l % 2) ^ (w % 2): each key's whole 128-byte row comes from 8 lanes
-  const int gk = ((lane >> 1) & 7) ^ (4 * ((lane >> 4) & 1));
-  const int gch = 2 * (lane >> 4) + ((lane & 1) ^ (wave & 1));
+  // ---- gathers: wave w fills chunk pairs w, w + 4, .. of every step; lane l of a
+  // block load writes 16-byte slot l of the block, i.e. key gk = (l / 2) ^ 4 (w % 2),
+  // chunk gc1 = (l % 2) ^ (gk / 8 % 2) of the pair.  The load's immediate offset
+  // (32 cp bytes) applies to the LDS address too, so M0 is pre-biased by -32 cp.
+  const int gk = (lane >> 1) ^ (4 * (wave & 1));
+  const int gc1 = (lane & 1) ^ ((gk >> 3) & 1);
   const uint32_t lds0 = (uint32_t)(size_t)(DSA_LDS unsigned char*)smem;
   const uint32_t rows_lds = lds0 + kW4Stages * STAGE;
   const int last_key = max(nkeys - 1, 0);
   // rows[] entry of this lane's gather key in step `step` (clamped inside the list)
-  auto row_read = [&](int step) -> int32_t {
-    return lds_read_b32(rows_lds + 4 * min(step * kKT + 8 * wave + gk, last_key));
+  auto row_read = [&](int step) -> int32_t { return lds_read_b32(rows_lds + 4 * min(step * kKT + gk, last_key)); };
+  auto row_ok = [&](int step, int32_t raw) -> int32_t { return step * kKT + gk < nkeys ? raw : -1; };
+  constexpr int R16 = DQK / 8;  // 16-byte records per KV row
+  const __amdgpu_buffer_rsrc_t kv_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)p.kv, (short)16, (int)p.buf_records, 0x00020000);
+  const uint16_t* const zero_src = g_zero_row + 8 * gc1;
+  const uint16_t* const kv_src = p.kv + 8 * gc1;
+  const uint16_t* const kv2_src = (p.kv2 ? p.kv2 : p.kv) + 8 * gc1;
+  // the load operand of row rr (-1: zeros): a record index (BUF) or a pointer
+  auto gather_src = [&](int32_t rr) {
+    if constexpr (BUF) {
+      return rr >= 0 ? (uint32_t)rr * (uint32_t)R16 + (uint32_t)gc1 : 0xffffffffu;
+    } else {
+      const uint16_t* base = (rr & dsa::kRowTag2) ? kv2_src : kv_src;
+      const uint16_t* src = base + (int64_t)(rr & ~dsa::kRowTag2) * DQK;
+      return rr >= 0 ? src : zero_src;
+    }
   };
-  auto row_ok = [&](int step, int32_t raw) -> int32_t { return step * kKT + 8 * wave + gk < nkeys ? raw : -1; };
-  // source of this lane's 16-byte loads for row rr (-1: the zero row), by selects
-  const uint16_t* const zero_src = g_zero_row + 8 * gch;
-  const uint16_t* const kv_src = p.kv + 8 * gch;
-  const uint16_t* const kv2_src = (p.kv2 ? p.kv2 : p.kv) + 8 * gch;
-  auto gather_src = [&](int32_t rr) -> const uint16_t* {
-    const uint16_t* base = (rr & dsa::kRowTag2) ? kv2_src : kv_src;
-    const uint16_t* src = base + (int64_t)(rr & ~dsa::kRowTag2) * DQK;
-    return rr >= 0 ? src : zero_src;
-  };
-  // The instruction's immediate offset (128 cg bytes) applies to both the global
-  // and the LDS address, so the LDS base passed in is pre-biased by -128 cg: one
-  // scalar add for M0 and no per-load address arithmetic.
-  auto issue_one = [&](int step, const uint16_t* src, auto C) {
-    constexpr int cg = decltype(C)::value;
+  using GSrc = decltype(gather_src(0));
+  const GSrc no_src = gather_src(-1);
+  auto issue_one = [&](int step, GSrc src, auto C) {
+    constexpr int cp = 4 * decltype(C)::value;  // + wave
     unsigned char* sb = smem + (step % kW4Stages) * STAGE + wave * 1024;
-    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (DSA_LDS void*)(sb + cg * (4096 - 128)), 16,
-                                     128 * cg, 0);
+    if constexpr (BUF)
+      buffer_load_lds16<32 * cp>(kv_rsrc, (DSA_LDS void*)(sb + cp * (1024 - 32)), src, 32 * wave);
+    else
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + 16 * wave),
+                                       (DSA_LDS void*)(sb + cp * (1024 - 32)), 16, 32 * cp, 0);
   };
-  auto issue = [&](int step, const uint16_t* src) {
+  auto issue = [&](int step, GSrc src) {
     static_for<0, NCG>([&](auto C) { issue_one(step, src, C); });
   };
   // rows[] entry of key l32 of step `step`, for its validity bit (clamped)
@@ -762,26 +780,20 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   };
 
   // ---- LDS read addresses (bytes from the start of a stage)
-  // score A fragment of k-step ks: key l32 (block kg = l32 / 8, key l32 % 8),
-  // chunk 2 ks + hh, at kq[ks % 4] + (ks / 4) * 4096
-  uint32_t kq[4];
-  {
-    const int kg = l32 >> 3, kr = l32 & 7;
+  // score A fragment of k-step ks: key l32, chunk 2 ks + hh (pair ks), at kq[ks % 2] + ks * 1024
+  uint32_t kq[2];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) kq[e] = kg * 1024 + w4_pos(kr, 2 * e + hh, kg);
-  }
+  for (int e = 0; e < 2; ++e) kq[e] = w4_pos(l32, e, hh) - 1024 * e;
   // P.V A fragment (d-tile dt, k-step kk), transposing read r (keys +8r): group
   // g = lane / 16 and lane sl = lane % 16 point at key 16 kk + 8 r + 4 hh + sl / 4,
-  // dims 32 dt + 16 (g % 2) + 4 (sl % 4) .. + 4, at vq[dt % 2][r] + (dt / 2) 4096 + kk 2048
-  uint32_t vq[2][2];
+  // dims 32 dt + 16 (g % 2) + 4 (sl % 4) .. + 4, i.e. chunk pair 2 dt + g % 2, at
+  // vq[r] + dt * 2048 + kk * 512
+  uint32_t vq[2];
   {
     const int g = (lane >> 4) & 3, sl = lane & 15;
-    const int vk = 4 * hh + (sl >> 2);
 #pragma unroll
-    for (int d2 = 0; d2 < 2; ++d2)
-#pragma unroll
-      for (int r2 = 0; r2 < 2; ++r2)
-        vq[d2][r2] = r2 * 1024 + w4_pos(vk, 4 * d2 + 2 * (g & 1) + ((sl & 3) >> 1), r2) + 8 * (sl & 1);
+    for (int r2 = 0; r2 < 2; ++r2)
+      vq[r2] = w4_pos(8 * r2 + 4 * hh + (sl >> 2), g & 1, (sl & 3) >> 1) + 8 * (sl & 1);
   }
 
   // ---- softmax state: lanes l32 and l32 + 32 share head l32
@@ -798,8 +810,8 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   auto v_read = [&](uint32_t vbase, auto F) {
     constexpr int f = decltype(F)::value;
     constexpr int dt = f >> 1, kk = f & 1;
-    vfr[f % kW4VPre][0] = lds_read_tr16<(dt >> 1) * 4096 + kk * 2048>(vbase + vq[dt & 1][0]);
-    vfr[f % kW4VPre][1] = lds_read_tr16<(dt >> 1) * 4096 + kk * 2048>(vbase + vq[dt & 1][1]);
+    vfr[f % kW4VPre][0] = lds_read_tr16<dt * 2048 + kk * 512>(vbase + vq[0]);
+    vfr[f % kW4VPre][1] = lds_read_tr16<dt * 2048 + kk * 512>(vbase + vq[1]);
   };
 
   // score product of the step in `sbase`: S^T = K . Q^T over KS k-steps, kW4KPre
@@ -807,20 +819,17 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   // first kW4VPre P.V fragments (of the stage at `vbase`) are read during the last
   // score MFMAs, whose K reads are already issued, so the P.V phase starts with
   // its operands in flight.
-  // Score accumulators and P^T by step parity: the softmax of step j starts in
-  // the shadow of the P.V MFMAs of step j - 1 (its maximum and the first half of
-  // its exponentials) and ends in the shadow of the score MFMAs of step j + 1, so
-  // that neither phase holds more than about eight instructions per 32-cycle
-  // MFMA (the issue rate of one wave).
+  // Score accumulators by step parity (the scores of step j accumulate while the
+  // exponentials of step j - 1 are taken) and P^T of the step whose P.V is next.
   f32x16 sacc[2];
-  dsa::i32x4 pbuf[2][2];  // P^T: the B operands of the two P.V k-steps
+  dsa::i32x4 pbuf[2];  // the B operands of the two P.V k-steps
   auto scores = [&](f32x16& acc, uint32_t sbase, uint32_t vbase, auto VPF, auto&& hook) {
     constexpr bool vpf = decltype(VPF)::value != 0;
     static_assert(kW4VPre <= kW4KPre, "the V prefetch uses the K-read slots of the last MFMAs");
     dsa::i32x4 kfr[kW4KPre];
     static_for<0, kW4KPre>([&](auto F) {
       constexpr int f = decltype(F)::value;
-      kfr[f] = lds_read_b128<(f / 4) * 4096>(sbase + kq[f % 4]);
+      kfr[f] = lds_read_b128<f * 1024>(sbase + kq[f & 1]);
     });
     static_for<0, KS>([&](auto F) {
       constexpr int f = decltype(F)::value;
@@ -830,7 +839,7 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
       lds_wait1<ky + 2 * vissued>(kfr[f % kW4KPre]);
       const dsa::i32x4 cur = kfr[f % kW4KPre];
       constexpr int fn = f + kW4KPre;
-      if constexpr (fn < KS) kfr[f % kW4KPre] = lds_read_b128<(fn / 4) * 4096>(sbase + kq[fn % 4]);
+      if constexpr (fn < KS) kfr[f % kW4KPre] = lds_read_b128<fn * 1024>(sbase + kq[fn & 1]);
       if constexpr (f == 0) mfma32_v0<F16>(acc, cur, qf[f]);
       else mfma32_v<F16>(acc, cur, qf[f]);
       if constexpr (vpf && f >= tail0 && f - tail0 < kW4VPre) v_read(vbase, IntC<f - tail0>{});
@@ -839,39 +848,41 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
     });
   };
 
-  // The softmax of one step (S^T in sc -> P^T in pb).  Pieces 1-6: maximum and
-  // reference-maximum update; pieces 7-23: exponential k = piece - 7 (< 16), then
-  // the sum and bf16 packing of exponential k - 1, so that no instruction reads
-  // the result of the transcendental just before it.  A raised reference only
-  // records alpha: O is rescaled once the P.V in flight (the previous step's, on
-  // the old reference) is done.
-  constexpr int kSoftPieces = 24;  // pieces 1 .. 23
-  constexpr int kSoftSplit = 15;   // pieces < kSoftSplit run beside the P.V MFMAs
+  // The softmax in pieces sized to the issue slots an MFMA leaves its wave: one
+  // 32-cycle MFMA window holds about two VALU operations beside a score MFMA and
+  // its fragment read, one beside a P.V MFMA and its two transposing reads (a
+  // transcendental counts twice).  Per step S:
+  //  * max_piece m = 0 .. 10, in the P.V windows of the step that computed S:
+  //    0-7 the lane's maximum (one v_max3 each), 8 the other half-wave's, 9 the
+  //    scale, 10 the reference update (which scales l_run and records alpha);
+  //  * exp_piece e = 0 .. 32, in the score windows of the next step: e = 2k takes
+  //    s_k * scale - mref (and, k even, packs exponentials k - 2, k - 1), e = 2k + 1
+  //    the exponential of k, e = 32 packs 14, 15;
+  //  * sum_piece k = 0 .. 15, in the P.V windows of the next step: l_run += p_k.
+  // A raised reference records alpha only: O is rescaled once the P.V in flight
+  // (the previous step's, on the old reference) is done.
+  constexpr int kMaxPieces = 11, kExpPieces = 33;
   float tmax = 0.f, mref = 0.f, alpha = 1.f;
   bool rescale = false;
-  auto softmax_piece = [&](f32x16& sc, dsa::i32x4 (&pb)[2], auto F) {
-    constexpr int f = decltype(F)::value;
-    if constexpr (f == 1) {
+  auto max_piece = [&](f32x16& sc, auto M) {
+    constexpr int m = decltype(M)::value;
+    if constexpr (m == 0) {
       tmax = max3(sc[0], sc[1], sc[2]);
-      tmax = max3(tmax, sc[3], sc[4]);
       pin(tmax);
-    } else if constexpr (f == 2) {
-      tmax = max3(tmax, sc[5], sc[6]);
-      tmax = max3(tmax, sc[7], sc[8]);
+    } else if constexpr (m >= 1 && m <= 6) {
+      tmax = max3(tmax, sc[2 * m + 1], sc[2 * m + 2]);
       pin(tmax);
-    } else if constexpr (f == 3) {
-      tmax = max3(tmax, sc[9], sc[10]);
-      tmax = max3(tmax, sc[11], sc[12]);
-      pin(tmax);
-    } else if constexpr (f == 4) {
-      tmax = max3(tmax, sc[13], sc[14]);
+    } else if constexpr (m == 7) {
       tmax = max3(tmax, sc[15], sc[15]);
       pin(tmax);
-    } else if constexpr (f == 5) {
+    } else if constexpr (m == 8) {
       const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-      tmax = max3(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1])) * p.scale_log2;
+      tmax = max3(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1]));
       pin(tmax);
-    } else if constexpr (f == 6) {
+    } else if constexpr (m == 9) {
+      tmax *= p.scale_log2;
+      pin(tmax);
+    } else if constexpr (m == 10) {
       // m_ref is a reference maximum, raised only when a score passes it by more
       // than 2^kSlack: probabilities exp2(s - m_ref) may reach 2^kSlack, which fp32
       // and bf16 carry with unchanged relative precision
@@ -884,27 +895,39 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
       }
       mref = m_ref == -__builtin_inff() ? 0.f : m_ref;
       pin(mref);
-    } else if constexpr (f >= 7 && f < kSoftPieces) {
-      constexpr int k = f - 7;
-      if constexpr (k < 16) {
-        float x = __builtin_amdgcn_exp2f(fmaf(sc[k], p.scale_log2, -mref));
-        pin(x);
-        sc[k] = x;
-      }
-      if constexpr (k >= 1) {
-        l_run += sc[k - 1];
-        pin(l_run);
-        if constexpr ((k - 1) & 1) {
-          int w = (int)dsa::pack_half2<F16>(sc[k - 2], sc[k - 1]);
-          pin(w);
-          pb[(k - 1) >> 3][((k - 1) & 7) >> 1] = w;
-        }
-      }
     }
   };
-  auto softmax_range = [&](f32x16& sc, dsa::i32x4 (&pb)[2], auto LO, auto HI) {
-    static_for<decltype(LO)::value, decltype(HI)::value>([&](auto F) { softmax_piece(sc, pb, F); });
+  auto pack = [&](f32x16& sc, dsa::i32x4 (&pb)[2], auto A) {
+    constexpr int a = decltype(A)::value;
+    int w = (int)dsa::pack_half2<F16>(sc[a], sc[a + 1]);
+    pin(w);
+    pb[a >> 3][(a & 7) >> 1] = w;
   };
+  auto exp_piece = [&](f32x16& sc, dsa::i32x4 (&pb)[2], auto E) {
+    constexpr int e = decltype(E)::value;
+    constexpr int k = e >> 1;
+    if constexpr (e < 32 && (e & 1) == 0) {
+      if constexpr (k >= 2 && (k & 1) == 0) pack(sc, pb, IntC<k - 2>{});
+      float x = fmaf(sc[k], p.scale_log2, -mref);
+      pin(x);
+      sc[k] = x;
+    } else if constexpr (e < 32) {
+      float x = __builtin_amdgcn_exp2f(sc[k]);
+      pin(x);
+      sc[k] = x;
+    } else if constexpr (e == 32) {
+      pack(sc, pb, IntC<14>{});
+    }
+  };
+  auto sum_piece = [&](f32x16& sc, auto K) {
+    l_run += sc[decltype(K)::value];
+    pin(l_run);
+  };
+  auto max_range = [&](f32x16& sc) { static_for<0, kMaxPieces>([&](auto M) { max_piece(sc, M); }); };
+  auto exp_range = [&](f32x16& sc, dsa::i32x4 (&pb)[2], auto LO) {
+    static_for<decltype(LO)::value, kExpPieces>([&](auto E) { exp_piece(sc, pb, E); });
+  };
+  auto sum_range = [&](f32x16& sc) { static_for<0, 16>([&](auto K) { sum_piece(sc, K); }); };
   // invalid keys (a partial step, -1 or masked indices; rare) score -inf.
   // Element r of this lane is key 8 (r / 4) + 4 hh + r % 4 of the step.
   auto apply_mask = [&](f32x16& sc, uint32_t vmask) {
@@ -938,8 +961,8 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
       constexpr int fn = f + kW4VPre;
       if constexpr (fn < 2 * ND) {
         constexpr int dn = fn >> 1, kn = fn & 1;
-        vfr[f % kW4VPre][0] = lds_read_tr16<(dn >> 1) * 4096 + kn * 2048>(sbase + vq[dn & 1][0]);
-        vfr[f % kW4VPre][1] = lds_read_tr16<(dn >> 1) * 4096 + kn * 2048>(sbase + vq[dn & 1][1]);
+        vfr[f % kW4VPre][0] = lds_read_tr16<dn * 2048 + kn * 512>(sbase + vq[0]);
+        vfr[f % kW4VPre][1] = lds_read_tr16<dn * 2048 + kn * 512>(sbase + vq[1]);
       }
       mfma32_o<dt, F16>(av, pp[kk]);
       hook(IntC<f>{});
@@ -957,13 +980,12 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   // ---- schedule.  Step j: wait for the gathers of step j, then the barrier
   // (stage j complete in every wave; stage j - 2 released by every wave), the
   // scores of j with the gathers of step j + 2 issued one chunk group every four
-  // MFMAs (a burst of loads stalls the issuing wave) and the second half of the
-  // softmax of j - 1, then the P.V of j - 1 with the first half of the softmax of
-  // j.  Stages in use at step j: j - 1 (P.V), j (scores), j + 1 and j + 2
-  // (loading).  The rows[] entries a step needs (its validity mask, the gather
-  // rows two steps ahead) are read one step early, ahead of the fragment reads
-  // whose waits cover them.  The loop is unrolled by two so that the parity
-  // buffers are registers.
+  // MFMAs (a burst of loads stalls the issuing wave) and the exponentials of
+  // j - 1, then the P.V of j - 1 with the sums of j - 1 and the maximum of j.
+  // Stages in use at step j: j - 1 (P.V), j (scores), j + 1 and j + 2 (loading).
+  // The rows[] entries a step needs (its validity mask, the gather rows two steps
+  // ahead) are read one step early, ahead of the fragment reads whose waits cover
+  // them.  The loop is unrolled by two so that the parity buffers are registers.
   int32_t row_raw = 0, mask_raw = 0;
   if (nsteps > 0) {
     int32_t r0 = row_read(0), r1 = row_read(1);
@@ -984,7 +1006,7 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
     // the last two steps load the zero row into idle stages instead of branching
     // around each load
     const bool more = j + 2 < nsteps;
-    const uint16_t* src = more ? gather_src(row_ok(j + 2, row_raw)) : zero_src;
+    const GSrc src = more ? gather_src(row_ok(j + 2, row_raw)) : no_src;
     if (wave_active) {
       const uint32_t sbase = lds0 + (j % kW4Stages) * STAGE;
       const uint32_t vbase = lds0 + ((j + kW4Stages - 1) % kW4Stages) * STAGE;  // stage of step j - 1
@@ -995,28 +1017,27 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
         });
         mfma_drain();
         apply_mask(sacc[P], vmask);
-        softmax_range(sacc[P], pbuf[P], IntC<1>{}, IntC<kSoftSplit>{});
+        max_range(sacc[P]);
+        rescale = false;  // O is still zero
       } else {
-        // gathers at MFMAs 1, 5, 9, ..; the softmax tail of j - 1 at 3, 7, 11, ..
+        // gathers at MFMAs 1, 5, 9, ..; exponential pieces of j - 1 after every MFMA
         scores(sacc[P], sbase, vbase, IntC<1>{}, [&](auto F) {
           constexpr int f = decltype(F)::value;
           if constexpr ((f & 3) == 1 && (f >> 2) < NCG) issue_one(j + 2, src, IntC<(f >> 2)>{});
-          if constexpr ((f & 3) == 3 && kSoftSplit + (f >> 2) < kSoftPieces)
-            softmax_piece(sacc[Q], pbuf[Q], IntC<kSoftSplit + (f >> 2)>{});
+          if constexpr (f < kExpPieces) exp_piece(sacc[Q], pbuf, IntC<f>{});
         });
         // pieces the score MFMAs had no room for (d_qk = 512)
-        constexpr int placed = kSoftSplit + KS / 4 < kSoftPieces ? kSoftSplit + KS / 4 : kSoftPieces;
-        softmax_range(sacc[Q], pbuf[Q], IntC<placed>{}, IntC<kSoftPieces>{});
+        constexpr int placed = KS < kExpPieces ? KS : kExpPieces;
+        exp_range(sacc[Q], pbuf, IntC<placed>{});
         mfma_drain();
         apply_mask(sacc[P], vmask);
-        // maximum at MFMAs 3 .. 8, then one exponential every other MFMA
-        pv(vbase, pbuf[Q], false, [&](auto F) {
+        // sums of j - 1 at MFMAs 0 .. 15, the maximum of j at 16 .. 26
+        pv(vbase, pbuf, false, [&](auto F) {
           constexpr int f = decltype(F)::value;
-          if constexpr (f >= 3 && f < 9) softmax_piece(sacc[P], pbuf[P], IntC<f - 2>{});
-          if constexpr (f >= 9 && ((f - 9) & 1) == 0 && 7 + (f - 9) / 2 < kSoftSplit)
-            softmax_piece(sacc[P], pbuf[P], IntC<7 + (f - 9) / 2>{});
+          if constexpr (f < 16) sum_piece(sacc[Q], IntC<f>{});
+          if constexpr (f >= 16 && f - 16 < kMaxPieces) max_piece(sacc[P], IntC<f - 16>{});
         });
-        static_assert(9 + 2 * (kSoftSplit - 8) <= 2 * ND, "the softmax head fits the P.V MFMAs");
+        static_assert(16 + kMaxPieces <= 2 * ND, "the softmax pieces fit the P.V MFMAs");
         apply_rescale();
       }
     } else {
@@ -1033,9 +1054,12 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   };
   auto last = [&](auto PAR) {  // the step nsteps - 1 has parity PAR
     constexpr int P = decltype(PAR)::value;
-    softmax_range(sacc[P], pbuf[P], IntC<kSoftSplit>{}, IntC<kSoftPieces>{});
+    exp_range(sacc[P], pbuf, IntC<0>{});
     valu_to_mfma();
-    pv(lds0 + ((nsteps - 1) % kW4Stages) * STAGE, pbuf[P], true, [](auto) {});
+    pv(lds0 + ((nsteps - 1) % kW4Stages) * STAGE, pbuf, true, [&](auto F) {
+      constexpr int f = decltype(F)::value;
+      if constexpr (f < 16) sum_piece(sacc[P], IntC<f>{});
+    });
   };
   if (nsteps > 0) step(0, IntC<0>{});
   int j = 1;
@@ -1209,15 +1233,29 @@ int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   return dsa::check_launch("dsa_sparse_mla_fwd");
 }
 
-template <int DQK, bool F16>
-int launch_mla_w4(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
+template <int DQK, bool F16, bool BUF>
+int launch_mla_w4_as(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   const size_t smem = (size_t)kW4Stages * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split;
-  auto fn = mla_w4_kernel<DQK, F16>;
+  auto fn = mla_w4_kernel<DQK, F16, BUF>;
   static std::atomic<int> lds_reserved[dsa::kMaxDevices];
   const int rc = dsa::reserve_lds((const void*)fn, smem, lds_reserved, "sparse_mla");
   if (rc != dsa::kOk) return rc;
   hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3(256), smem, stream, p);
   return dsa::check_launch("dsa_sparse_mla_fwd");
+}
+
+template <int DQK, bool F16>
+int launch_mla_w4(MlaParams p, int64_t nblocks, hipStream_t stream) {
+  // rows of the pool: a page pool (or resolved rows), or B sequences of skv rows
+  const int64_t rows = (p.block_table || p.direct) ? p.pool_rows : (int64_t)p.B * p.skv;
+  // the buffer's byte offsets are 32-bit: pools of at most 4 GiB
+  const int64_t records = rows * (DQK / 8);
+  if (p.kv2 == nullptr && records * 16 <= ((int64_t)1 << 32)) {
+    p.buf_records = (uint32_t)records;
+    return launch_mla_w4_as<DQK, F16, true>(p, nblocks, stream);
+  }
+  p.buf_records = 0u;
+  return launch_mla_w4_as<DQK, F16, false>(p, nblocks, stream);
 }
 
 // Workgroup form.  More than 64 heads: the 4-wave, 128-head form (one
