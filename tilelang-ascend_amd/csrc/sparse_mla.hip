@@ -146,6 +146,8 @@ __device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, 
       idx[r] = p.topk > 0 ? __builtin_nontemporal_load(ip + min(kbeg + tid + r * NT, p.topk - 1)) : -1;
 #pragma unroll
     for (int r = 0; r < R; ++r) idx[r] = tid + r * NT < nkeys ? idx[r] : -1;
+    // paged: the page-table loads go out ahead of mid()'s loads (memory results
+    // retire in issue order, so loads issued before them would delay the table)
     mid();
     if (p.direct) {
       // resolved rows: bit 30 selects the second pool
@@ -714,6 +716,13 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   const int kbeg = split * p.keys_per_split;
   const int nkeys = max(0, min(p.keys_per_split, p.topk - kbeg));
 
+  // O^T = 0 and the sink load before any other memory operation: the compiler
+  // waits for every load in flight ahead of an asm block naming the accumulation
+  // registers, and for all earlier loads ahead of a load's first use.
+  zero_o();
+  const float sink_log2 =
+      p.sink != nullptr && split == 0 && head_ok ? p.sink[head] * dsa::kLog2e : -__builtin_inff();
+
   // ---- Q^T operand of k-step ks: head l32, dims 16 ks + 8 hh .. + 8.  Loaded
   // behind the index loads of the list and ahead of their use, so the query
   // fetch overlaps the row resolution and the first gathers; the first score
@@ -724,10 +733,8 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const dsa::i32x4*>(qp + 16 * ks);
   });
-  if (!head_ok) {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = dsa::i32x4{0, 0, 0, 0};
-  }
+  // (a lane past the last head computes with head 0's query; its column of S, P
+  // and O is never written out, and no other head's column depends on it)
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // rows[] written
   __builtin_amdgcn_s_barrier();                        // ... by every wave
 
@@ -796,14 +803,11 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
       vq[r2] = w4_pos(8 * r2 + 4 * hh + (sl >> 2), g & 1, (sl & 3) >> 1) + 8 * (sl & 1);
   }
 
-  // ---- softmax state: lanes l32 and l32 + 32 share head l32
-  float m_ref = -__builtin_inff();
-  float l_run = 0.f;
-  if (p.sink != nullptr && split == 0 && head_ok) {
-    m_ref = p.sink[head] * dsa::kLog2e;
-    l_run = hh == 0 ? 1.f : 0.f;
-  }
-  zero_o();
+  // ---- softmax state: lanes l32 and l32 + 32 share head l32 (the sink was
+  // loaded first thing: a load issued after the query loads would hold its use,
+  // and the ring fill behind it, until the query had arrived)
+  float m_ref = sink_log2;
+  float l_run = m_ref == -__builtin_inff() ? 0.f : (hh == 0 ? 1.f : 0.f);
 
   // P.V A fragments in flight: fragment f = 2 dt + kk, two transposing reads
   dsa::i32x2 vfr[kW4VPre][2];

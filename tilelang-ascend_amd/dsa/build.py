@@ -9,6 +9,7 @@ library travels with the source tree.  Run ``python -m dsa.build`` (with
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -49,6 +50,31 @@ def _compile(src: Path, obj: Path) -> None:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
 
 
+def _check_accumulators() -> None:
+    """The 4-wave sparse MLA keeps O in the accumulation registers (AGPRs), which
+    only its inline asm names; the compiler must not place any value of its own
+    there.  Fails the build if the device assembly of those kernels holds a
+    compiler-generated v_accvgpr_* instruction."""
+    src = CSRC / "sparse_mla.hip"
+    asm = BUILD_DIR / "sparse_mla.s"
+    cmd = [hipcc(), *COMMON_FLAGS, "-I", str(CSRC), "-x", "hip", "--cuda-device-only", "-S", str(src),
+           "-o", str(asm)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed for {src.name}:\n{res.stderr}")
+    text = asm.read_text()
+    bad = []
+    for m in re.finditer(r"^(_ZN\w*mla_w4_kernel\w*):", text, re.M):
+        end = text.index(".Lfunc_end", m.start())
+        n = sum(1 for line in text[m.start():end].splitlines()
+                if line.strip().startswith("v_accvgpr_") and "Ldsa_acc" not in line)
+        if n:
+            bad.append(f"{m.group(1)}: {n}")
+    if bad:
+        raise RuntimeError("compiler-allocated accumulation registers in the 4-wave sparse MLA "
+                           "(they hold O there):\n" + "\n".join(bad))
+
+
 def build(verbose: bool = False, jobs: int = 8) -> Path:
     """Compile every HIP source for gfx950 and link the shared library."""
     BUILD_DIR.mkdir(exist_ok=True)
@@ -60,7 +86,10 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
         objs.append(obj)
         work.append((src, obj))
     with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(work)))) as ex:
-        list(ex.map(lambda sw: _compile(*sw), work))
+        futs = [ex.submit(_compile, *sw) for sw in work]
+        futs.append(ex.submit(_check_accumulators))
+        for fut in futs:
+            fut.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
