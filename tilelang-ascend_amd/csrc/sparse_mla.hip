@@ -375,11 +375,12 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
         }
       if (vmask != 0xffffffffu) {
         tmax = -__builtin_inff();
+        const uint32_t m = vmask >> (4 * g);  // one variable shift; constant bit tests below
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            if (!((vmask >> (16 * kt + 4 * g + i)) & 1u)) sv[kt][i] = -__builtin_inff();
+            if (!((m >> (16 * kt + i)) & 1u)) sv[kt][i] = -__builtin_inff();
             tmax = fmaxf(tmax, sv[kt][i]);
           }
       }
