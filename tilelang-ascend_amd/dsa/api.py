@@ -538,13 +538,14 @@ def sparse_attn_tilelang(query: torch.Tensor, key: torch.Tensor, value: torch.Te
     else:
         q = query.unsqueeze(0).contiguous()
         kv = key.contiguous()
-    act_q = int(actual_seq_lengths_query.reshape(-1)[0])
+    # the lengths stay on the device (no host round trip): the causal start and
+    # the rows past the query length are formed there
+    act_q = actual_seq_lengths_query.reshape(1).to(device=dev, dtype=torch.int32)
     act_kv = actual_seq_lengths_kv.reshape(1).to(device=dev, dtype=torch.int32)
     idx = sparse_indices.to(device=dev, dtype=torch.int32).contiguous().view(1, T, 1, -1)
     out = sparse_mla_fwd(q, kv, idx, float(scale_value), block_table=block_table, seq_len_kv=act_kv,
                          q_start_index_s=act_kv - act_q, is_causal=True, return_lse=False)[0]
-    if act_q < T:
-        out[max(act_q, 0):].zero_()
+    out.mul_((torch.arange(T, device=dev, dtype=torch.int32) < act_q).view(T, 1, 1))
     return out
 
 
@@ -743,22 +744,23 @@ def sparse_flash_mla(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[
     # the small tensors (tables, lengths, sinks, lists) may live anywhere: they are
     # moved to q's device, as sparse_flash_mla_api.py:186-214 does
     dev = _require_gpu(q, ori_kv, cmp_kv)
+    # query lengths and row offsets are formed on the device (no host round trip)
     if layout_q == "TND":
         assert cu_seqlens_q is not None, "cu_seqlens_q is required for TND"
-        cu = cu_seqlens_q.to(torch.int64).cpu()
+        cu = cu_seqlens_q.reshape(-1).to(device=dev, dtype=torch.int32)
         B = cu.numel() - 1
         T, N1, D = q.shape
-        seq_lens = (cu[1:] - cu[:-1]).tolist()
-        q_prefix = cu[:-1].to(torch.int32)
+        act_q = (cu[1:] - cu[:-1]).contiguous()
+        q_prefix = cu[:-1].contiguous()
         S_max = None
     else:
         B, S_max, N1, D = q.shape
         T = B * S_max
-        q_prefix = torch.arange(B, dtype=torch.int32) * S_max
-        seq_lens = [S_max] * B
+        q_prefix = torch.arange(B, dtype=torch.int32, device=dev) * S_max
+        act_q = torch.full((B,), S_max, dtype=torch.int32, device=dev)
         if cu_seqlens_q is not None:
-            cu = cu_seqlens_q.to(torch.int64).cpu()
-            seq_lens = (cu[1:] - cu[:-1]).tolist()
+            cu = cu_seqlens_q.reshape(-1).to(device=dev, dtype=torch.int32)
+            act_q = (cu[1:] - cu[:-1]).contiguous()
     N2 = ori_kv.shape[2]
     if scenario == 3:
         ci = cmp_sparse_indices.to(torch.int32)
@@ -781,8 +783,7 @@ def sparse_flash_mla(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[
         _require_contiguous(name, t)
     ori_bt = ori_block_table.to(device=dev, dtype=torch.int32).contiguous()
     cmp_bt = cmp_block_table.to(device=dev, dtype=torch.int32).contiguous() if cmp_kv is not None else None
-    act_q = torch.tensor(seq_lens, dtype=torch.int32, device=dev)
-    qp = q_prefix.to(dev)
+    qp = q_prefix
     kvl = seqused_kv.to(device=dev, dtype=torch.int32).contiguous()
     sk = sinks.to(device=dev, dtype=torch.float32).contiguous()
     out = torch.empty((T, N1, D), dtype=q.dtype, device=dev)
