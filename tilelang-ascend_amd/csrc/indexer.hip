@@ -85,8 +85,86 @@ __device__ __forceinline__ int visible_keys(int t, int aq, int ak, int sparse_mo
   return ak;
 }
 
-__device__ __forceinline__ float fp8_to_f32(uint32_t byte) {
-  return __builtin_amdgcn_cvt_f32_fp8((int)byte, 0);
+// Maximum over the 64 lanes of a wave, in every lane: DPP quad permutes and
+// row mirrors within each row of 16 lanes, then the permlane swaps across rows
+// (no LDS round trip; max is exact, so the combining order does not matter).
+template <int CTL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp_f32<0xB1>(x));   // quad_perm [1,0,3,2]
+  x = fmaxf(x, dpp_f32<0x4E>(x));   // quad_perm [2,3,0,1]
+  x = fmaxf(x, dpp_f32<0x141>(x));  // row_half_mirror
+  x = fmaxf(x, dpp_f32<0x140>(x));  // row_mirror
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+}
+
+// u/2 = sum_h (w_h / 2) q_h of one token, for the u MFMA.  token_u_load issues
+// the query loads: lane (r, cc) = (lane >> 4, lane & 15) takes heads 16r ..
+// 16r+15, bytes 8cc .. 8cc+7 of each (sixteen 8-byte loads, all in flight).
+// token_u_sum forms the partial sums of those heads for the 8 dims with the
+// token's weights (wl: its 64 weights, staged in LDS), and a reduce-scatter over
+// the four lane rows (permlane swaps) leaves lane (r, cc) the totals of dims
+// 8cc + 2r and 8cc + 2r + 1, returned in u0, u1 (the function returns that
+// first dim).  Every dim's total is (rows 0 + 2) + (rows 1 + 3).  The sums are
+// taken as sum_h w_h q_h and halved at the end, which rounds exactly as the
+// sum of (w_h / 2) q_h does (a power-of-two scale commutes with rounding,
+// subnormal results aside).
+__device__ __forceinline__ void token_u_load(const uint8_t* qtok, int lane, dsa::i32x2 (&qv)[16]) {
+  const uint8_t* qp = qtok + 16 * (lane >> 4) * kDim + 8 * (lane & 15);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) qv[j] = *reinterpret_cast<const dsa::i32x2*>(qp + j * kDim);
+}
+
+__device__ __forceinline__ int token_u_sum(const dsa::i32x2 (&qv)[16], const float* wl, int lane, float& u0,
+                                           float& u1) {
+  const int r = lane >> 4, cc = lane & 15;
+  dsa::f32x4 wv[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) wv[k] = *reinterpret_cast<const dsa::f32x4*>(wl + 16 * r + 4 * k);
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float w = wv[j >> 2][j & 3];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(qv[j][hf], false);  // bytes 0, 1
+      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(qv[j][hf], true);   // bytes 2, 3
+      a[4 * hf + 0] = fmaf(w, lo[0], a[4 * hf + 0]);
+      a[4 * hf + 1] = fmaf(w, lo[1], a[4 * hf + 1]);
+      a[4 * hf + 2] = fmaf(w, hi[0], a[4 * hf + 2]);
+      a[4 * hf + 3] = fmaf(w, hi[1], a[4 * hf + 3]);
+    }
+  }
+  // rows 0, 1 keep dims 0..3 of their 8, rows 2, 3 dims 4..7 (pairs of rows 0-2, 1-3)
+  float b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[i]), __float_as_uint(a[4 + i]), false, false);
+    b[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  // row r keeps dims 2r, 2r + 1 (pairs of rows 0-1, 2-3)
+  float t[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(b[i]), __float_as_uint(b[2 + i]), false, false);
+    t[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  u0 = 0.5f * t[0];
+  u1 = 0.5f * t[1];
+  return 8 * cc + 2 * r;
+}
+
+// Makes this wave's LDS writes visible to its own later LDS reads of other
+// lanes' entries (the compiler may not move such reads above the writes).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Waits until at most n of this wave's vector-memory operations are in flight
@@ -136,6 +214,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   // fall on distinct banks
   __shared__ __align__(16) uint8_t usplit[kWaves][kSplits][kDim + 16];
   __shared__ int uexp[kWaves];
+  __shared__ __align__(16) float wsh[kWaves][kHeads];  // each token's weights
   __shared__ __align__(16) float lin[2][kWaves][kKeyTile];  // u.k per token and key, two tiles
 
   // XCD-aware mapping: the work items (key group (b, chunk), token block), key
@@ -146,7 +225,8 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   const int xcd = bid % dsa::kNumXcd, r = bid / dsa::kNumXcd;
   const int64_t witem = (int64_t)xcd * p.per_xcd + r;
   if (r >= p.per_xcd || witem >= (int64_t)p.B * p.nkc * p.ntb) return;
-  const int kg = (int)(witem / p.ntb), tb = (int)(witem % p.ntb);
+  // the host bounds the grid (hence witem) below 2^31: 32-bit division
+  const int kg = (int)witem / p.ntb, tb = (int)witem % p.ntb;
   const int b = kg / p.nkc, kc = kg % p.nkc;
 
   // Rows of batch b: varlen (prefix sums) or padded [B, S1] / [B, S2].
@@ -172,11 +252,13 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   const int g = lane >> 4, c = lane & 15;
 
   // Key range of this workgroup: its chunk, clipped to what its tokens can see.
-  int lmax = 0;
-  for (int i = 0; i < kTokPerBlock; ++i) {
-    const int t = tb * kTokPerBlock + i;
-    if (t < p.S1) lmax = max(lmax, visible_keys(t, aq, ak, p.sparse_mode));
-  }
+  // visible_keys is ak over a leading run of tokens (mode 3, cl <= 0), then
+  // nondecreasing up to aq, then 0, so its maximum over the block's tokens
+  // [t0, t1) lies at t0 or t1 - 1
+  const int t0 = tb * kTokPerBlock;
+  const int t1 = min(min(t0 + kTokPerBlock, p.S1), aq);
+  const int lmax =
+      t0 < t1 ? max(visible_keys(t0, aq, ak, p.sparse_mode), visible_keys(t1 - 1, aq, ak, p.sparse_mode)) : 0;
   const int k0 = kc * p.chunk;
   const int kend = min(k0 + p.chunk, p.S2);  // last key this workgroup may write
   const int k1 = min(kend, lmax);            // last key any token needs
@@ -188,78 +270,6 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   if (kc == 0 && p.row_len != nullptr && lane == 0 && tok_ok) p.row_len[qbase + tok] = L;
   if (k0 >= k1) return;
   const int64_t trow = qbase + (tok_ok ? tok : 0);
-
-  // ---- per-token operands -------------------------------------------------
-  // q: lane (g, c) holds head 16*mt + c, bytes [32g, 32g+32) of the head.
-  dsa::i32x8 qa[4];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const dsa::i32x4* src =
-        reinterpret_cast<const dsa::i32x4*>(p.q + (trow * kHeads + 16 * mt + c) * kDim + 32 * g);
-    const dsa::i32x4 lo = tok_ok ? src[0] : dsa::i32x4{0, 0, 0, 0};
-    const dsa::i32x4 hi = tok_ok ? src[1] : dsa::i32x4{0, 0, 0, 0};
-    qa[mt] = dsa::i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  }
-  // w/2 for the heads whose |q.k| this lane's accumulators hold (16mt + 4g + i).
-  float wh[4][4];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) wh[mt][i] = tok_ok ? 0.5f * p.w[trow * kHeads + 16 * mt + 4 * g + i] : 0.f;
-
-  // u/2 = sum_h (w_h / 2) q_h: lane l computes dims 2l and 2l+1.
-  float u0 = 0.f, u1 = 0.f;
-  if (tok_ok) {
-    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(p.q + trow * kHeads * kDim) + lane;
-    const float* wrow = p.w + trow * kHeads;
-#pragma unroll 8
-    for (int h = 0; h < kHeads; ++h) {
-      const uint32_t two = qrow[h * (kDim / 2)];
-      const float wv = 0.5f * wrow[h];
-      u0 = fmaf(wv, fp8_to_f32(two & 0xff), u0);
-      u1 = fmaf(wv, fp8_to_f32(two >> 8), u1);
-    }
-  }
-  // Power-of-two split of u: sigma_s = 2^(e - 4s) with max|u| / 2^e in (224, 448].
-  float umax = fmaxf(fabsf(u0), fabsf(u1));
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) umax = fmaxf(umax, __shfl_xor(umax, d, 64));
-  int e = -100;
-  if (umax > 0.f) {
-    int ex;
-    (void)frexpf(umax / (float)kE4m3Max, &ex);  // umax/448 = f * 2^ex, f in [0.5, 1)
-    e = clampi(ex, -100, 100);
-  }
-  if (lane == 0) uexp[wave] = e;
-  if constexpr (PAGED) {
-    // physical pool row of every key of the chunk (-1: page outside the pool)
-    for (int i = tid; i < k1 - k0; i += kThreads) {
-      const int key = k0 + i;
-      const int blk = key / p.block_size;
-      const int pg = blk < p.max_blocks ? p.block_table[(int64_t)b * p.max_blocks + blk] : -1;
-      const int64_t row = (int64_t)pg * p.block_size + key % p.block_size;
-      krows[i] = (pg >= 0 && row < p.pool_rows) ? (int32_t)row : -1;
-    }
-  }
-  {
-    float r0 = u0, r1 = u1;
-#pragma unroll
-    for (int sp = 0; sp < kSplits; ++sp) {
-      const float inv = ldexpf(1.f, 4 * sp - e), sig = ldexpf(1.f, e - 4 * sp);
-      const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(r0 * inv, r1 * inv, 0, false);
-      *reinterpret_cast<uint16_t*>(&usplit[wave][sp][2 * lane]) = (uint16_t)pk;
-      r0 = fmaf(-sig, __builtin_amdgcn_cvt_f32_fp8(pk, 0), r0);
-      r1 = fmaf(-sig, __builtin_amdgcn_cvt_f32_fp8(pk, 1), r1);
-    }
-  }
-  __syncthreads();
-  // u pieces of the group's 4 tokens as A rows: row 4*tq + sp = piece sp of token
-  // grp0 + tq; lane (g, c) holds row c, bytes 32g..32g+31.  In the result, lane
-  // (g, c) then holds the 4 pieces (rows 4g..4g+3) of token grp0 + g for key c.
-  // The operand stays in LDS (read once per tile, where it is used).
-  const int grp0 = wave & ~3, ublk = wave & 3;
-  const uint32_t ua_addr = lds_addr(&usplit[grp0 + (c >> 2)][c & 3][32 * g]);
-  const int uscale = clampi(127 + uexp[grp0 + (c >> 2)] - 4 * (c & 3), 1, 254);
 
   // ---- key tiles ------------------------------------------------------------
   const int ntiles = (k1 - k0 + kKeyTile - 1) / kKeyTile;
@@ -285,6 +295,87 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
       __builtin_amdgcn_global_load_lds(src, (DSA_LDS void*)&kscale[t & (kStages - 1)][0], 4, 0, 0);
     }
   };
+  // ---- per-token operands -------------------------------------------------
+  // Row trow exists (a workgroup that reaches this point has a valid token, so
+  // its batch has row qbase): every load below is issued unconditionally, and a
+  // wave past the batch's tokens zeroes its weights and A operands once they
+  // arrive (loads behind a wave-uniform condition would become branches that
+  // each wait for their load).  First the u sums' operands (the token's 64
+  // weights, one per lane, copied into LDS, and the query bytes in the u sums'
+  // layout); the ring's first tiles and the A operands are requested while the
+  // sums are formed.
+  const int qkeep = tok_ok ? -1 : 0;
+  __builtin_amdgcn_global_load_lds(p.w + trow * kHeads + lane, (DSA_LDS void*)&wsh[wave][0], 4, 0, 0);
+  dsa::i32x2 qv[16];
+  token_u_load(p.q + trow * kHeads * kDim, lane, qv);
+  dsa::wait_vmcnt<0>();
+  wave_lds_sync();
+  // u/2 = sum_h (w_h / 2) q_h: lane (r, cc) ends with dims udim and udim + 1.
+  float u0 = 0.f, u1 = 0.f;
+  int udim = 2 * lane;
+  if (tok_ok) udim = token_u_sum(qv, &wsh[wave][0], lane, u0, u1);
+  // w/2 for the heads whose |q.k| this lane's accumulators hold (16mt + 4g + i).
+  float wh[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const dsa::f32x4 v = *reinterpret_cast<const dsa::f32x4*>(&wsh[wave][16 * mt + 4 * g]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wh[mt][i] = __int_as_float(__float_as_int(0.5f * v[i]) & qkeep);
+  }
+  // Contiguous keys: the ring's first tiles (paged keys need the chunk's rows
+  // first, below).
+  if constexpr (!PAGED) {
+#pragma unroll
+    for (int i = 0; i < kStages - 1; ++i) issue(i);
+  }
+  // q: lane (g, c) holds head 16*mt + c, bytes [32g, 32g+32) of the head.
+  dsa::i32x8 qa[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const dsa::i32x4* src =
+        reinterpret_cast<const dsa::i32x4*>(p.q + (trow * kHeads + 16 * mt + c) * kDim + 32 * g);
+    const dsa::i32x4 lo = src[0], hi = src[1];
+    qa[mt] = dsa::i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  // Power-of-two split of u: sigma_s = 2^(e - 4s) with max|u| / 2^e in (224, 448].
+  const float umax = wave_max(fmaxf(fabsf(u0), fabsf(u1)));
+  int e = -100;
+  if (umax > 0.f) {
+    int ex;
+    (void)frexpf(umax / (float)kE4m3Max, &ex);  // umax/448 = f * 2^ex, f in [0.5, 1)
+    e = clampi(ex, -100, 100);
+  }
+  if (lane == 0) uexp[wave] = e;
+  if constexpr (PAGED) {
+    // physical pool row of every key of the chunk (-1: page outside the pool)
+    for (int i = tid; i < k1 - k0; i += kThreads) {
+      const int key = k0 + i;
+      const int blk = key / p.block_size;
+      const int pg = blk < p.max_blocks ? p.block_table[(int64_t)b * p.max_blocks + blk] : -1;
+      const int64_t row = (int64_t)pg * p.block_size + key % p.block_size;
+      krows[i] = (pg >= 0 && row < p.pool_rows) ? (int32_t)row : -1;
+    }
+  }
+  {
+    float r0 = u0, r1 = u1;
+#pragma unroll
+    for (int sp = 0; sp < kSplits; ++sp) {
+      const float inv = ldexpf(1.f, 4 * sp - e), sig = ldexpf(1.f, e - 4 * sp);
+      const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(r0 * inv, r1 * inv, 0, false);
+      *reinterpret_cast<uint16_t*>(&usplit[wave][sp][udim]) = (uint16_t)pk;
+      r0 = fmaf(-sig, __builtin_amdgcn_cvt_f32_fp8(pk, 0), r0);
+      r1 = fmaf(-sig, __builtin_amdgcn_cvt_f32_fp8(pk, 1), r1);
+    }
+  }
+  __syncthreads();
+  // u pieces of the group's 4 tokens as A rows: row 4*tq + sp = piece sp of token
+  // grp0 + tq; lane (g, c) holds row c, bytes 32g..32g+31.  In the result, lane
+  // (g, c) then holds the 4 pieces (rows 4g..4g+3) of token grp0 + g for key c.
+  // The operand stays in LDS (read once per tile, where it is used).
+  const int grp0 = wave & ~3, ublk = wave & 3;
+  const uint32_t ua_addr = lds_addr(&usplit[grp0 + (c >> 2)][c & 3][32 * g]);
+  const int uscale = clampi(127 + uexp[grp0 + (c >> 2)] - 4 * (c & 3), 1, 254);
+
   // B-operand reads: lane (g, c) reads key 16blk + c, chunks 2g and 2g+1.
   const int rslot = (2 * g) ^ (c & 7) ^ (c >> 3);
   const uint32_t rd0 = lds_addr(&ktile[0][0]) + c * kDim + 16 * rslot;
@@ -308,6 +399,10 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
       want_gmax ? p.gmax + trow * p.ld_g + k0 / 16 : p.logits, (short)0,
       (want_gmax && tok_ok) ? ((kend - k0 + 15) / 16) * 4 : 0, 0x00020000);
 
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qa[mt][j] &= qkeep;
   // the u pieces' A operand, read once (loop invariant)
   dsa::i32x8 ua;
   {
@@ -315,11 +410,14 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
     lds_wait2<0>(u0, u1);
     ua = dsa::i32x8{u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
   }
-  // The operand loads above complete before the ring starts, so the only vector
-  // memory operations in flight inside the loop are the ring's and the stores.
-  dsa::wait_vmcnt<0>();
+  // The operand loads above complete before the loop (their values were used,
+  // and loads complete in issue order), so the only vector memory operations in
+  // flight inside the loop are the ring's and the stores.
+  if constexpr (PAGED) {
+    dsa::wait_vmcnt<0>();
 #pragma unroll
-  for (int i = 0; i < kStages - 1; ++i) issue(i);
+    for (int i = 0; i < kStages - 1; ++i) issue(i);
+  }
 
   // u.k hand-off: this wave writes block ublk of its group's 4 tokens, reads its own token.
   const uint32_t lin_wr = lds_addr(&lin[0][grp0 + g][16 * ublk + c]);
@@ -490,6 +588,7 @@ constexpr int kDecMaxChunk = 2048;
 template <bool PAGED, bool SCALED>
 __global__ __launch_bounds__(kDecWaves * 64) void indexer_decode_kernel(IndexerParams p) {
   __shared__ __align__(16) uint8_t upieces[kDecWaves][kSplits][kDim];
+  __shared__ __align__(16) float dwsh[kDecWaves][kHeads];
   __shared__ int32_t drows[PAGED ? kDecWaves : 1][PAGED ? kDecMaxChunk : 1];
 
   const int lane = threadIdx.x & 63;
@@ -526,6 +625,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void indexer_decode_kernel(IndexerP
   const int k1 = min(kend, L);
   if (k0 >= k1) return;
 
+  // operands as in the kernel above: weights (one per lane, shared through
+  // LDS), the u sums' query bytes, then the A operands
+  const float wl = p.w[trow * kHeads + lane];
+  dsa::i32x2 qv[16];
+  token_u_load(p.q + trow * kHeads * kDim, lane, qv);
   // q: lane (g, c) holds head 16 mt + c, bytes [32g, 32g+32).
   dsa::i32x8 qa[4];
 #pragma unroll
@@ -535,28 +639,20 @@ __global__ __launch_bounds__(kDecWaves * 64) void indexer_decode_kernel(IndexerP
     const dsa::i32x4 hi = *reinterpret_cast<const dsa::i32x4*>(src + 16);
     qa[mt] = dsa::i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
+  dwsh[wave][lane] = wl;
+  wave_lds_sync();
   float wh[4][4];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < 4; ++mt) {
+    const dsa::f32x4 v = *reinterpret_cast<const dsa::f32x4*>(&dwsh[wave][16 * mt + 4 * g]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wh[mt][i] = 0.5f * p.w[trow * kHeads + 16 * mt + 4 * g + i];
-
-  // u/2 = sum_h (w_h / 2) q_h (lane l: dims 2l, 2l+1) and its fp8 pieces, as above.
-  float u0 = 0.f, u1 = 0.f;
-  {
-    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(p.q + trow * kHeads * kDim) + lane;
-    const float* wrow = p.w + trow * kHeads;
-#pragma unroll 8
-    for (int h = 0; h < kHeads; ++h) {
-      const uint32_t two = qrow[h * (kDim / 2)];
-      const float wv = 0.5f * wrow[h];
-      u0 = fmaf(wv, fp8_to_f32(two & 0xff), u0);
-      u1 = fmaf(wv, fp8_to_f32(two >> 8), u1);
-    }
+    for (int i = 0; i < 4; ++i) wh[mt][i] = 0.5f * v[i];
   }
-  float umax = fmaxf(fabsf(u0), fabsf(u1));
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) umax = fmaxf(umax, __shfl_xor(umax, d, 64));
+
+  // u/2 = sum_h (w_h / 2) q_h and its fp8 pieces, as above.
+  float u0, u1;
+  const int udim = token_u_sum(qv, &dwsh[wave][0], lane, u0, u1);
+  const float umax = wave_max(fmaxf(fabsf(u0), fabsf(u1)));
   int e = -100;
   if (umax > 0.f) {
     int ex;
@@ -569,7 +665,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void indexer_decode_kernel(IndexerP
     for (int sp = 0; sp < kSplits; ++sp) {
       const float inv = ldexpf(1.f, 4 * sp - e), sig = ldexpf(1.f, e - 4 * sp);
       const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(r0 * inv, r1 * inv, 0, false);
-      *reinterpret_cast<uint16_t*>(&upieces[wave][sp][2 * lane]) = (uint16_t)pk;
+      *reinterpret_cast<uint16_t*>(&upieces[wave][sp][udim]) = (uint16_t)pk;
       r0 = fmaf(-sig, __builtin_amdgcn_cvt_f32_fp8(pk, 0), r0);
       r1 = fmaf(-sig, __builtin_amdgcn_cvt_f32_fp8(pk, 1), r1);
     }

@@ -136,11 +136,13 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hh = lane >> 5, l32 = lane & 31;
 
-  int lmax = 0;
-  for (int i = 0; i < kHTokPerBlock; ++i) {
-    const int t = tb * kHTokPerBlock + i;
-    if (t < p.S1) lmax = max(lmax, visible_keys(t, aq, ak, p.sparse_mode));
-  }
+  // visible_keys is ak over a leading run of tokens (mode 3, cl <= 0), then
+  // nondecreasing up to aq, then 0, so its maximum over the block's tokens
+  // [t0, t1) lies at t0 or t1 - 1
+  const int t0 = tb * kHTokPerBlock;
+  const int t1 = min(min(t0 + kHTokPerBlock, p.S1), aq);
+  const int lmax =
+      t0 < t1 ? max(visible_keys(t0, aq, ak, p.sparse_mode), visible_keys(t1 - 1, aq, ak, p.sparse_mode)) : 0;
   const int k0 = kc * p.chunk;
   const int kend = min(k0 + p.chunk, p.S2);
   const int k1 = min(kend, lmax);
