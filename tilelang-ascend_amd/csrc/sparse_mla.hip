@@ -105,8 +105,10 @@ __device__ __align__(16) uint16_t g_zero_row[576];
 // Physical row of each index of this split (-1 = skip): rows[j] for key kbeg + j of
 // the token's list, after the validity rules (range, page, causal) or the
 // DeepSeek-V4 key-set generation.  All NT threads of the workgroup take part.
-// mid() runs once the list's index loads are issued and before any is used, so
-// loads it issues (the query operands) overlap the resolution.
+// mid() runs once the list's own loads (indices, lengths, page table) are issued,
+// so loads it issues (the query operands) overlap the resolution without
+// delaying it: memory results retire in issue order, so a query load issued
+// ahead of a page-table load would make the table wait for the query.
 struct NoMid {
   __device__ void operator()() const {}
 };
@@ -146,10 +148,10 @@ __device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, 
       idx[r] = p.topk > 0 ? __builtin_nontemporal_load(ip + min(kbeg + tid + r * NT, p.topk - 1)) : -1;
 #pragma unroll
     for (int r = 0; r < R; ++r) idx[r] = tid + r * NT < nkeys ? idx[r] : -1;
-    // paged: the page-table loads go out ahead of mid()'s loads (memory results
-    // retire in issue order, so loads issued before them would delay the table)
-    mid();
+    // the compiler may not hoist mid()'s loads above the list's loads
+    asm volatile("" ::: "memory");
     if (p.direct) {
+      mid();
       // resolved rows: bit 30 selects the second pool
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -167,12 +169,19 @@ __device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, 
       if (p.causal) ok[r] = ok[r] && idx[r] <= qs + s;
     }
     if (p.block_table) {
+      // table entries at clamped positions (max_blocks > 0), loaded without a
+      // branch per load, ahead of mid()'s loads; their values are taken only
+      // after mid() (a wait for them is not hoisted above its loads)
+      const int32_t* bt = p.block_table + (int64_t)b * p.max_blocks;
       int page[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int blk = idx[r] / p.block_size;
-        page[r] = ok[r] && blk < p.max_blocks ? p.block_table[(int64_t)b * p.max_blocks + blk] : -1;
-      }
+      for (int r = 0; r < R; ++r) page[r] = bt[min(max(idx[r], 0) / p.block_size, p.max_blocks - 1)];
+      asm volatile("" ::: "memory");
+      mid();
+#pragma unroll
+      for (int r = 0; r < R; ++r) asm volatile("" : "+v"(page[r]) : : "memory");
+#pragma unroll
+      for (int r = 0; r < R; ++r) page[r] = ok[r] && idx[r] / p.block_size < p.max_blocks ? page[r] : -1;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int j = tid + r * NT;
@@ -180,6 +189,7 @@ __device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, 
         if (j < nkeys) rows[j] = page[r] >= 0 && rr < p.pool_rows ? (int32_t)rr : -1;
       }
     } else {
+      mid();
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int j = tid + r * NT;
