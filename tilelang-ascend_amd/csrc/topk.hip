@@ -44,6 +44,9 @@ constexpr int kSortThreads = kThreads;
 constexpr int kSampleBlocks = 128; // 64-element blocks sampled from a long row
 constexpr int kBucketMax = 256;    // largest bucket the bucket ordering ranks directly
 
+// A readable zero word: the load target of an absent optional array.
+__device__ float g_zero_word;
+
 __device__ __forceinline__ uint32_t ordered_key(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) == 0u) u = 0u;                                       // -0.0 -> +0.0
@@ -424,11 +427,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ITEMS 
   const int64_t row = blockIdx.x;
   const float* xr = a.x + row * a.ld;
   const int K = a.K;
-  int L = a.cols;
-  if (a.row_len != nullptr) {
-    int r = a.row_len[row];
-    L = r < 0 ? 0 : (r < a.cols ? r : a.cols);
+  // The row's length and (streamed rows with group maxima) its first
+  // kSampleBlocks * 64 group maxima are requested together, unconditionally and
+  // at clamped positions (an absent array reads a zero word), so that neither
+  // waits for the other; entries past the row's groups are masked where used.
+  constexpr int kPerG = kSampleBlocks * 64 / kThreads;
+  const bool gm_ok = a.gmax != nullptr && a.ld_g > 0;
+  const float* gp = gm_ok ? a.gmax + row * a.ld_g : &g_zero_word;
+  const int glim = gm_ok ? (int)(a.ld_g < 0x7fffffff ? a.ld_g : 0x7fffffff) - 1 : 0;
+  const int r_raw = *(a.row_len != nullptr ? a.row_len + row : reinterpret_cast<const int32_t*>(&g_zero_word));
+  float gpre[ITEMS == 0 ? kPerG : 1];
+  if constexpr (ITEMS == 0) {
+#pragma unroll
+    for (int u = 0; u < kPerG; ++u) gpre[u] = gp[min(tid + u * kThreads, glim)];
   }
+  int L = a.cols;
+  if (a.row_len != nullptr) L = r_raw < 0 ? 0 : (r_raw < a.cols ? r_raw : a.cols);
   if (tid == 0) {
     sh->cnt[0] = 0u;
     sh->cnt[1] = 0u;
@@ -561,12 +575,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ITEMS 
       if (use_g || (L >= 8 * K && nb >= 16)) {
         uint32_t sv[kPer];
         uint32_t smin = 0xffffffffu, smax = 0u;
-        const float* grow = use_g ? a.gmax + row * a.ld_g : nullptr;
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
           const int i = tid + u * kThreads;
           if (use_g) {
-            sv[u] = i < ns ? ordered_key(grow[i]) : 0u;
+            sv[u] = i < ns ? ordered_key(gpre[u]) : 0u;
           } else {
             const int blk = i >> 6;
             const int start = (int)(((int64_t)blk * L / nb) & ~63);
