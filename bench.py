@@ -291,7 +291,8 @@ def summarize_profile(root: str) -> str:
         f"WRITE_SIZE x {calib.get('WRITE_SIZE', float('nan')):.4f} bytes per KiB read / 1024",
         "# role: median over the role's dispatches (trace_mean/min/max_us: mean, min, max of its kernel-trace "
         "durations); mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x "
-        "GRBM_GUI_ACTIVE / 8); clock_ghz = GRBM_GUI_ACTIVE / 8 / trace_us",
+        "GRBM_GUI_ACTIVE / 8); clock_ghz = GRBM_GUI_ACTIVE / 8 / trace_us (the counter's clock domain: near the "
+        "shader clock for the long kernels, above it for short ones, up to past the 2.4 GHz shader maximum)",
     ]
     for role in ("indexer", "topk", "mla", "mla_combine", "dec_indexer", "dec_topk", "dec_mla", "dec_mla_combine",
                  "config3_mla", "config3_mla_combine"):
