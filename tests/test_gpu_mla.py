@@ -52,6 +52,28 @@ def test_minus_one_padding_and_sentinel(gpu):
     assert torch.count_nonzero(out[0, 6]) == 0 and torch.isinf(lse[0, 6]).all()
 
 
+@pytest.mark.parametrize("S,topk,q_start", [(320, 256, 0), (3, 64, 0), (40, 64, 30), (24, 64, 100)])
+def test_128_heads_short_causal_rows(gpu, S, topk, q_start):
+    # one causal sequence through the 128-head form: the rows whose list ends in
+    # -1 padding stop after their last valid key, and the short rows are dealt to
+    # the XCDs apart from the long ones; holes, front padding, a row with nothing
+    # valid and indices past the causal bound must all keep their meaning
+    inp = inputs.mla_prefill(B=1, S=S, Skv=q_start + S, H=128, topk=topk, seed=17, q_start=q_start)
+    idx = inp["indices"]
+    g = torch.Generator().manual_seed(5)
+    holes = torch.rand(idx.shape, generator=g) < 0.1
+    idx[holes] = -1
+    r = min(S - 1, 2)
+    idx[0, r, 0, :] = -1                      # nothing to attend to
+    if S > 10:
+        row = idx[0, 9, 0].clone()
+        idx[0, 9, 0, :] = -1
+        idx[0, 9, 0, -4:] = row[:4]           # valid keys only at the end of the list
+        idx[0, 10, 0, -1] = q_start + 11      # past the causal bound: masked
+    out, lse = _check(inp, gpu, is_causal=True, q_start_index_s=q_start)
+    assert torch.count_nonzero(out[0, r]) == 0 and torch.isinf(lse[0, r]).all()
+
+
 def test_causal_mask_applies(gpu):
     inp = inputs.mla_prefill(B=1, S=16, Skv=512, H=16, topk=64, seed=13)
     g = torch.Generator().manual_seed(0)

@@ -71,6 +71,7 @@ struct MlaParams {
   int B, S, H, topk;
   int block_size, max_blocks;
   int nsplit, keys_per_split, nhg;
+  int balance;                  // token order balanced for short causal rows (balanced_token)
   uint32_t buf_records;         // 16-byte records of the KV pool (buffer-addressed gathers of the 4-wave form)
   float scale_log2;
   int causal;
@@ -105,6 +106,9 @@ __device__ __align__(16) uint16_t g_zero_row[576];
 // Physical row of each index of this split (-1 = skip): rows[j] for key kbeg + j of
 // the token's list, after the validity rules (range, page, causal) or the
 // DeepSeek-V4 key-set generation.  All NT threads of the workgroup take part.
+// Returns the largest j this thread wrote with a valid row (-1: none), so that
+// the caller can stop after the last valid key instead of stepping through the
+// -1 padding of a short list.
 // mid() runs once the list's own loads (indices, lengths, page table) are issued,
 // so loads it issues (the query operands) overlap the resolution without
 // delaying it: memory results retire in issue order, so a query load issued
@@ -113,7 +117,7 @@ struct NoMid {
   __device__ void operator()() const {}
 };
 template <int NT, typename Mid = NoMid>
-__device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, int b, int s, int kbeg, int nkeys,
+__device__ __forceinline__ int resolve_rows(const MlaParams& p, int64_t token, int b, int s, int kbeg, int nkeys,
                                              int32_t* rows, int tid, Mid mid = Mid{}) {
   if (p.v4_on) {
     mid();
@@ -131,7 +135,12 @@ __device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, 
       __syncthreads();
     }
     const int stop = v4_sh[1];
-    for (int j = tid; j < nkeys; j += NT) rows[j] = vb >= 0 ? dsa::v4_row(p.v4, token, vb, kbeg + j, stop) : -1;
+    int last = -1;
+    for (int j = tid; j < nkeys; j += NT) {
+      rows[j] = vb >= 0 ? dsa::v4_row(p.v4, token, vb, kbeg + j, stop) : -1;
+      if (rows[j] >= 0) last = j;
+    }
+    return last;
   } else {
     // every index load of the thread is issued before any is used, then every
     // page-table load: two memory round trips for the whole list instead of one
@@ -150,6 +159,7 @@ __device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, 
     for (int r = 0; r < R; ++r) idx[r] = tid + r * NT < nkeys ? idx[r] : -1;
     // the compiler may not hoist mid()'s loads above the list's loads
     asm volatile("" ::: "memory");
+    int last = -1;
     if (p.direct) {
       mid();
       // resolved rows: bit 30 selects the second pool
@@ -159,8 +169,9 @@ __device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, 
         const int rr = idx[r] & ~dsa::kRowTag2;
         const bool ok = idx[r] >= 0 && (int64_t)rr < ((idx[r] & dsa::kRowTag2) ? p.pool_rows2 : p.pool_rows);
         if (j < nkeys) rows[j] = ok ? idx[r] : -1;
+        if (j < nkeys && ok) last = j;
       }
-      return;
+      return last;
     }
     bool ok[R];
 #pragma unroll
@@ -186,7 +197,9 @@ __device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, 
       for (int r = 0; r < R; ++r) {
         const int j = tid + r * NT;
         const int64_t rr = (int64_t)page[r] * p.block_size + idx[r] % p.block_size;
-        if (j < nkeys) rows[j] = page[r] >= 0 && rr < p.pool_rows ? (int32_t)rr : -1;
+        const bool okr = page[r] >= 0 && rr < p.pool_rows;
+        if (j < nkeys) rows[j] = okr ? (int32_t)rr : -1;
+        if (j < nkeys && okr) last = j;
       }
     } else {
       mid();
@@ -194,9 +207,30 @@ __device__ __forceinline__ void resolve_rows(const MlaParams& p, int64_t token, 
       for (int r = 0; r < R; ++r) {
         const int j = tid + r * NT;
         if (j < nkeys) rows[j] = ok[r] ? (int32_t)((int64_t)b * p.skv + idx[r]) : -1;
+        if (j < nkeys && ok[r]) last = j;
       }
     }
+    return last;
   }
+}
+
+// Token of workgroup (xcd, rq) when p.balance is set (one sequence, one split, one
+// head group, causal).  Token s of the chunk has at most min(topk, qs + s + 1)
+// valid keys, so the first s_short = clamp(topk - 1 - qs, 0, S) tokens have short
+// lists, which the kernel ends after their last valid key.  The long tokens are
+// cut into 8 equal contiguous ranges, one per XCD (neighbouring tokens' index sets
+// overlap in one L2), and the short ones are dealt round-robin after them, so the
+// XCDs get equal work.  -1: no token (the grid has up to 8 spare workgroups).
+__device__ __forceinline__ int64_t balanced_token(const MlaParams& p, int xcd, int rq) {
+  const int64_t kvl = p.kv_len ? (int64_t)p.kv_len[0] : p.skv;
+  const int64_t qs = p.q_start ? (int64_t)p.q_start[0] : kvl - p.S;
+  const int s_short = (int)min((int64_t)p.S, max((int64_t)0, (int64_t)p.topk - 1 - qs));
+  const int nl = p.S - s_short;
+  const int per_l = (nl + dsa::kNumXcd - 1) / dsa::kNumXcd;
+  const int nlx = max(0, min(per_l, nl - xcd * per_l));
+  if (rq < nlx) return (int64_t)s_short + (int64_t)xcd * per_l + rq;
+  const int64_t sh = (int64_t)dsa::kNumXcd * (rq - nlx) + xcd;
+  return sh < s_short ? sh : -1;
 }
 
 // 16-head-per-wave form.  A ring stage is 36 (or 32) blocks of 1 KB; block (key
@@ -258,7 +292,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
   const bool wave_active = hg * HPG + wave * 16 < p.H;
 
   const int kbeg = split * p.keys_per_split;
-  const int nkeys = max(0, min(p.keys_per_split, p.topk - kbeg));
+  const int nlist = max(0, min(p.keys_per_split, p.topk - kbeg));  // list entries of this split
 
   // ---- Q^T operand: lane (g, c) holds head c, dims 64(ks/2) + 16g + 8(ks%2) .. +8,
   // i.e. 16-byte chunk 8(ks/2) + 2g + ks%2 (the chunk order the K reads use; any
@@ -272,10 +306,19 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
                        : dsa::i32x4{0, 0, 0, 0};
   }
 
-  // ---- resolve this split's indices to physical rows (-1 = skip) ----
-  resolve_rows<NT>(p, token, b, s, kbeg, nkeys, rows, tid);
+  // ---- resolve this split's indices to physical rows (-1 = skip); the list
+  // ends after its last valid key (steps past it would add exactly nothing) ----
+  int last_ok = resolve_rows<NT>(p, token, b, s, kbeg, nlist, rows, tid);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) last_ok = max(last_ok, __shfl_xor(last_ok, o));
+  int32_t* const last_slot = rows + p.keys_per_split;  // one per wave
+  if (lane == 0) last_slot[wave] = last_ok;
   wait_vmcnt<0>();  // Q operands are in registers before any gather is queued
-  __syncthreads();  // rows[] ready
+  __syncthreads();  // rows[] and last_slot[] ready
+  int nk = -1;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) nk = max(nk, last_slot[w]);
+  const int nkeys = __builtin_amdgcn_readfirstlane(nk + 1);
 
   // ---- gather of step `step` into ring stage step % kStages.  Wave w fills the
   // blocks (kg = w % 4, cg = CGS i + w / 4), i = 0, 1, ...; lane l loads in-block
@@ -712,8 +755,14 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   const int64_t T = (int64_t)p.B * p.S;
   const int64_t units = T * p.nsplit;
   const int64_t per_xcd = (units + dsa::kNumXcd - 1) / dsa::kNumXcd;
-  const int64_t x = (int64_t)xcd * per_xcd + rq / p.nhg;
-  if (x >= units || rq / p.nhg >= per_xcd) return;
+  int64_t x;
+  if (p.balance) {
+    x = balanced_token(p, xcd, rq);
+    if (x < 0) return;
+  } else {
+    x = (int64_t)xcd * per_xcd + rq / p.nhg;
+    if (x >= units || rq / p.nhg >= per_xcd) return;
+  }
   const int64_t token = x / p.nsplit;
   const int split = (int)(x % p.nsplit);
   const int b = (int)(token / p.S), s = (int)(token % p.S);
@@ -725,7 +774,7 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   const bool head_ok = head < p.H;
   const bool wave_active = hg * kHeadsPerGroup + wave * 32 < p.H;
   const int kbeg = split * p.keys_per_split;
-  const int nkeys = max(0, min(p.keys_per_split, p.topk - kbeg));
+  const int nlist = max(0, min(p.keys_per_split, p.topk - kbeg));  // list entries of this split
 
   // O^T = 0 and the sink load before any other memory operation: the compiler
   // waits for every load in flight ahead of an asm block naming the accumulation
@@ -739,15 +788,23 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   // fetch overlaps the row resolution and the first gathers; the first score
   // MFMA waits for it together with the gathers of step 0.
   dsa::i32x4 qf[KS];
-  resolve_rows<NT>(p, token, b, s, kbeg, nkeys, rows, tid, [&]() {
+  int last_ok = resolve_rows<NT>(p, token, b, s, kbeg, nlist, rows, tid, [&]() {
     const uint16_t* qp = p.q + (token * p.H + (head_ok ? head : 0)) * DQK + 8 * hh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const dsa::i32x4*>(qp + 16 * ks);
   });
   // (a lane past the last head computes with head 0's query; its column of S, P
   // and O is never written out, and no other head's column depends on it)
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // rows[] written
+  // The list ends after its last valid key: the steps past it (the -1 padding of
+  // a short causal row) would add exactly nothing.
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) last_ok = max(last_ok, __shfl_xor(last_ok, o));
+  int32_t* const last_slot = rows + p.keys_per_split;  // one per wave
+  if (lane == 0) last_slot[wave] = last_ok;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // rows[] and last_slot[] written
   __builtin_amdgcn_s_barrier();                        // ... by every wave
+  const int nkeys = __builtin_amdgcn_readfirstlane(
+      max(max(last_slot[0], last_slot[1]), max(last_slot[2], last_slot[3])) + 1);
 
   // ---- gathers: wave w fills chunk pairs w, w + 4, .. of every step; lane l of a
   // block load writes 16-byte slot l of the block, i.e. key gk = (l / 2) ^ 4 (w % 2),
@@ -1239,7 +1296,8 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const uint16_t* __rest
 
 template <int DQK, int STAGES, int WAVES, bool F16>
 int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
-  const size_t smem = (size_t)STAGES * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split;
+  // ring, the rows[] list, one last-valid-key slot per wave
+  const size_t smem = (size_t)STAGES * kKT * DQK * 2 + sizeof(int32_t) * ((size_t)p.keys_per_split + WAVES);
   auto fn = sparse_mla_kernel<DQK, STAGES, WAVES, F16>;
   static std::atomic<int> lds_reserved[dsa::kMaxDevices];
   const int rc = dsa::reserve_lds((const void*)fn, smem, lds_reserved, "sparse_mla");
@@ -1250,7 +1308,8 @@ int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
 
 template <int DQK, bool F16, bool BUF>
 int launch_mla_w4_as(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
-  const size_t smem = (size_t)kW4Stages * kKT * DQK * 2 + sizeof(int32_t) * (size_t)p.keys_per_split;
+  // ring, the rows[] list, one last-valid-key slot per wave
+  const size_t smem = (size_t)kW4Stages * kKT * DQK * 2 + sizeof(int32_t) * ((size_t)p.keys_per_split + 4);
   auto fn = mla_w4_kernel<DQK, F16, BUF>;
   static std::atomic<int> lds_reserved[dsa::kMaxDevices];
   const int rc = dsa::reserve_lds((const void*)fn, smem, lds_reserved, "sparse_mla");
@@ -1261,6 +1320,12 @@ int launch_mla_w4_as(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
 
 template <int DQK, bool F16>
 int launch_mla_w4(MlaParams p, int64_t nblocks, hipStream_t stream) {
+  // one causal sequence in one split: short rows spread over the XCDs
+  // (balanced_token), whose grid needs up to 8 more workgroups
+  if (p.B == 1 && p.nsplit == 1 && p.nhg == 1 && p.causal && !p.v4_on && !p.direct && p.topk > 0) {
+    p.balance = 1;
+    nblocks = ((int64_t)p.S + dsa::kNumXcd - 1) / dsa::kNumXcd * dsa::kNumXcd + dsa::kNumXcd;
+  }
   // rows of the pool: a page pool (or resolved rows), or B sequences of skv rows
   const int64_t rows = (p.block_table || p.direct) ? p.pool_rows : (int64_t)p.B * p.skv;
   // the buffer's byte offsets are 32-bit: pools of at most 4 GiB
@@ -1354,6 +1419,7 @@ int sparse_mla_run(const MlaRun& r, const char* what) {
   p.max_blocks = r.max_blocks;
   p.scale_log2 = r.sm_scale * kLog2e;
   p.causal = r.is_causal;
+  p.balance = 0;
 
   p.nhg = (r.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
   int ns = r.num_splits > 0 ? r.num_splits : choose_splits(T, p.nhg, r.topk);
