@@ -192,7 +192,8 @@ def _profile_roles(dispatches):
     """Label the DSA kernels of a --profile-run in dispatch order.  A layer step
     launches indexer, topk, mla, dec_indexer, dec_topk, dec_mla in that order (a
     combine after an MLA with split partials takes the MLA's role + "_combine");
-    an MLA launched where a layer step would start is a config-3 decode."""
+    an MLA launched where a layer step would start is a config-3 decode, or the
+    config-4 prefill when no combine follows it."""
     seq = ("indexer", "topk", "mla", "dec_indexer", "dec_topk", "dec_mla")
 
     def cat(name):
@@ -222,6 +223,12 @@ def _profile_roles(dispatches):
         roles.append(role)
         if role is not None:
             prev = role
+    # an MLA outside a layer step with no combine after it is the config-4 prefill
+    for i, role in enumerate(roles):
+        if role == "config3_mla":
+            nxt = next((r for r in roles[i + 1:] if r is not None), None)
+            if nxt != "config3_mla_combine":
+                roles[i] = "config4_mla"
     return roles
 
 
@@ -265,12 +272,18 @@ def summarize_profile(root: str) -> str:
 
     vals = {}
     calib = {}
+    # the 1 GiB device copy at the start of the run is the largest copy dispatch
+    # (input set-up issues smaller ones later)
+    biggest = {}
     for rows in counters.values():
         for _, name, c in rows:
             if "copyBuffer" in name:
                 for cname in ("FETCH_SIZE", "WRITE_SIZE"):
-                    if cname in c and c[cname] > 100000:
-                        calib[cname] = 1073741824.0 / (c[cname] * 1024.0)
+                    if cname in c and c[cname] > biggest.get(cname, 100000):
+                        biggest[cname] = c[cname]
+    for cname, v in biggest.items():
+        calib[cname] = 1073741824.0 / (v * 1024.0)
+    for rows in counters.values():
         for role, lst in by_role(rows, lambda r: r[2]).items():
             for c in lst:
                 for cname, v in c.items():
@@ -278,7 +291,7 @@ def summarize_profile(root: str) -> str:
     dur = by_role(traces, lambda r: r[2] / 1000.0)
     lines = [
         "# rocprofv3 summary of bench.py --profile-run (1 GiB device copy, config 5 layer step x 13 = the bench's "
-        "3 warmup + 10 timed steps, config 3 decode x 3)",
+        "3 warmup + 10 timed steps, config 3 decode x 3, config 4 prefill x 15)",
         "# made on one MI355X (repo root R, after cd /tmp && export TMPDIR=/tmp), one rocprofv3 run per line:",
         f"#   rocprofv3 --pmc {' '.join(PROFILE_PASSES[0])} -d R/gpurun_out/prof/p1 -o run --output-format csv "
         "-- python3 R/bench.py --profile-run",
@@ -295,7 +308,7 @@ def summarize_profile(root: str) -> str:
         "shader clock for the long kernels, above it for short ones, up to past the 2.4 GHz shader maximum)",
     ]
     for role in ("indexer", "topk", "mla", "mla_combine", "dec_indexer", "dec_topk", "dec_mla", "dec_mla_combine",
-                 "config3_mla", "config3_mla_combine"):
+                 "config3_mla", "config3_mla_combine", "config4_mla"):
         if role not in vals and role not in dur:
             continue
         m = {k: statistics.median(v) for k, v in vals.get(role, {}).items()}
@@ -377,6 +390,37 @@ def read_profile(path: str) -> dict:
     return out
 
 
+def prefill_config4(L, runs: int, warmup: int = 10) -> dict:
+    """Config 4, sparse-MLA prefill: Sq = Skv = 16384 causal, H = 128, top-2048 (row
+    i draws from [0, i], -1 padded); mean microseconds per launch after `warmup`
+    launches (the shader clock under this 7.6 ms kernel settles only after about
+    ten launches in a process; the first ones run up to 10 % slower)."""
+    import torch
+
+    from dsa import inputs
+
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream(dev).cuda_stream
+    p = inputs.mla_prefill(B=1, S=16384, Skv=16384, H=H, topk=TOPK, seed=4, q_start=0, device=dev)
+    S = p["q"].shape[1]
+    out = torch.empty((1, S, H, DV), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((1, S, H), dtype=torch.float32, device=dev)
+    qs = torch.zeros((1,), dtype=torch.int32, device=dev)
+
+    def pre():
+        rc = L.dsa_sparse_mla_fwd(p["q"].data_ptr(), p["kv"].data_ptr(), p["indices"].data_ptr(), None, None,
+                                  qs.data_ptr(), None, 1, S, H, DQK, DV, S, 0, 0, TOPK, DQK ** -0.5, 1, 1,
+                                  out.data_ptr(), lse.data_ptr(), None, 0, st)
+        if rc != 0:
+            raise RuntimeError(f"prefill: {L.dsa_last_error().decode()}")
+
+    us = _time_launches(pre, runs, warmup=warmup)
+    fl = mla_flops(S)
+    del p, out, lse
+    return {"us": round(us, 1), "tflops": round(fl / us / 1e6, 1),
+            "frac_of_bf16_peak": round(fl / us / 1e6 / PEAK_BF16_TFLOPS, 4)}
+
+
 def target_configs(L, steps: int) -> dict:
     """The single-kernel north-star shapes beside the layer step: sparse-MLA decode
     (B=64, 64K paged context) and prefill (Sq=Skv=16384), and indexer + top-k at
@@ -398,24 +442,7 @@ def target_configs(L, steps: int) -> dict:
     torch.cuda.empty_cache()
 
     # config 4: prefill, Sq = Skv = 16384, causal index ranges, top-2048
-    p = inputs.mla_prefill(B=1, S=16384, Skv=16384, H=H, topk=TOPK, seed=4, q_start=0, device=dev)
-    S = p["q"].shape[1]
-    out = torch.empty((1, S, H, DV), dtype=torch.bfloat16, device=dev)
-    lse = torch.empty((1, S, H), dtype=torch.float32, device=dev)
-    qs = torch.zeros((1,), dtype=torch.int32, device=dev)
-
-    def pre():
-        chk(L.dsa_sparse_mla_fwd(p["q"].data_ptr(), p["kv"].data_ptr(), p["indices"].data_ptr(), None, None,
-                                 qs.data_ptr(), None, 1, S, H, DQK, DV, S, 0, 0, TOPK, DQK ** -0.5, 1, 1,
-                                 out.data_ptr(), lse.data_ptr(), None, 0, st), "prefill")
-
-    # steady state: the shader clock under this 7.6 ms kernel settles only after
-    # about ten launches in a process (the first ones run up to 10 % slower)
-    us = _time_launches(pre, max(2, steps // 2), warmup=10)
-    fl = mla_flops(S)
-    res["prefill_16k"] = {"us": round(us, 1), "tflops": round(fl / us / 1e6, 1),
-                          "frac_of_bf16_peak": round(fl / us / 1e6 / PEAK_BF16_TFLOPS, 4)}
-    del p, out, lse
+    res["prefill_16k"] = prefill_config4(L, runs=max(2, steps // 2))
     torch.cuda.empty_cache()
 
     # config 2: indexer + top-k, 4096 x 32768
@@ -791,9 +818,11 @@ def main() -> int:
         del layer
         torch.cuda.empty_cache()
         decode_config3(lib_handle, runs=3)
+        torch.cuda.empty_cache()
+        prefill_config4(lib_handle, runs=5, warmup=10)
         torch.cuda.synchronize()
         print(f"profile run: copy of 1073741824 bytes, {args.warmup + args.steps} layer steps, three config-3 "
-              "decodes", flush=True)
+              "decodes, fifteen config-4 prefills", flush=True)
         return 0
     for _ in range(args.warmup):
         layer.step()

@@ -23,3 +23,18 @@ def test_help_lists_contract_flags():
     assert r.returncode == 0
     for flag in ("--gpus", "--steps", "--warmup"):
         assert flag in r.stdout
+
+
+def test_profile_roles_label_the_dispatch_order():
+    # a layer step (prefill indexer, top-k, MLA; decode indexer, top-k, MLA with a
+    # combine), then a config-3 decode (MLA + combine) and config-4 prefills (MLA
+    # with no combine): the labels the counter summary groups the dispatches by
+    sys.path.insert(0, ROOT)
+    import bench
+
+    names = ["indexer_fp8_kernel", "copy_kernel", "topk_rows_kernel", "mla_w4_kernel", "indexer_fp8_kernel",
+             "topk_rows_kernel", "mla_w4_kernel", "mla_combine_kernel", "mla_w4_kernel", "mla_combine_kernel",
+             "mla_w4_kernel", "mla_w4_kernel"]
+    assert bench._profile_roles(names) == [
+        "indexer", None, "topk", "mla", "dec_indexer", "dec_topk", "dec_mla", "dec_mla_combine",
+        "config3_mla", "config3_mla_combine", "config4_mla", "config4_mla"]
