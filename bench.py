@@ -234,7 +234,9 @@ def _profile_roles(dispatches):
 
 PROFILE_PASSES = (("GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16",
                    "SQ_INSTS_VALU_MFMA_MOPS_F8", "SQ_INSTS_VALU_MFMA_MOPS_F6F4", "SQ_INSTS_MFMA", "SQ_WAVES"),
-                  ("FETCH_SIZE",), ("WRITE_SIZE",))
+                  ("FETCH_SIZE",), ("WRITE_SIZE",),
+                  ("SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_WAIT_INST_LDS", "SQ_INSTS_VALU",
+                   "SQ_INSTS_SALU", "SQ_WAVE_CYCLES", "SQ_WAIT_ANY"))
 
 
 def summarize_profile(root: str) -> str:
@@ -297,6 +299,7 @@ def summarize_profile(root: str) -> str:
         "-- python3 R/bench.py --profile-run",
         "#   rocprofv3 --pmc FETCH_SIZE -d R/gpurun_out/prof/p2 ... (same)",
         "#   rocprofv3 --pmc WRITE_SIZE -d R/gpurun_out/prof/p3 ... (same)",
+        f"#   rocprofv3 --pmc {' '.join(PROFILE_PASSES[3])} -d R/gpurun_out/prof/p4 ... (same)",
         "#   rocprofv3 --kernel-trace --stats -d R/gpurun_out/prof/kt -o run --output-format csv -- python3 "
         "R/bench.py --profile-run",
         "#   python3 R/bench.py --summarize-profile R/gpurun_out/prof",
@@ -305,7 +308,9 @@ def summarize_profile(root: str) -> str:
         "# role: median over the role's dispatches (trace_mean/min/max_us: mean, min, max of its kernel-trace "
         "durations); mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x "
         "GRBM_GUI_ACTIVE / 8); clock_ghz = GRBM_GUI_ACTIVE / 8 / trace_us (the counter's clock domain: near the "
-        "shader clock for the long kernels, above it for short ones, up to past the 2.4 GHz shader maximum)",
+        "shader clock for the long kernels, above it for short ones, up to past the 2.4 GHz shader maximum); "
+        "lds_bank_conflict_frac = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE; lds_wait_frac = SQ_WAIT_INST_LDS / "
+        "SQ_WAVE_CYCLES",
     ]
     for role in ("indexer", "topk", "mla", "mla_combine", "dec_indexer", "dec_topk", "dec_mla", "dec_mla_combine",
                  "config3_mla", "config3_mla_combine", "config4_mla"):
@@ -334,7 +339,12 @@ def summarize_profile(root: str) -> str:
             out["write_bytes"] = float(f"{m['WRITE_SIZE'] * 1024 * calib['WRITE_SIZE']:.4e}")
         if "fetch_bytes" in out and "write_bytes" in out:
             out["hbm_bytes"] = float(f"{out['fetch_bytes'] + out['write_bytes']:.4e}")
-        for cname in ("SQ_INSTS_MFMA", "SQ_WAVES", "SQ_BUSY_CU_CYCLES", "GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES"):
+        if m.get("SQ_LDS_IDX_ACTIVE"):
+            out["lds_bank_conflict_frac"] = round(m.get("SQ_LDS_BANK_CONFLICT", 0.0) / m["SQ_LDS_IDX_ACTIVE"], 4)
+        if m.get("SQ_WAVE_CYCLES"):
+            out["lds_wait_frac"] = round(m.get("SQ_WAIT_INST_LDS", 0.0) / m["SQ_WAVE_CYCLES"], 4)
+        for cname in ("SQ_INSTS_MFMA", "SQ_WAVES", "SQ_BUSY_CU_CYCLES", "GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES",
+                      *PROFILE_PASSES[3]):
             if cname in m:
                 out[cname] = float(f"{m[cname]:.5e}")
         lines.append(f"role={role} " + " ".join(f"{k}={v}" for k, v in out.items() if v is not None))
