@@ -506,6 +506,8 @@ def target_configs(L, steps: int) -> dict:
     del kb, k8, ks, qb, wq, q8, wo
     torch.cuda.empty_cache()
     res["indexer_decode"] = indexer_decode_configs(L, steps)
+    res["indexer_h16_128k"] = indexer_h16_config(L, steps)
+    res["bench_sfa_decode"] = bench_sfa_configs(L, steps)
     res["flash_mla_v4"] = flash_mla_v4_configs(L, steps)
     res["block_sparse_indexer"] = block_sparse_indexer_configs(L, steps)
     res["fp8_producers"] = {"key_cache_128k_us": round(uk, 2),
@@ -580,6 +582,117 @@ def block_sparse_indexer_configs(L, steps: int) -> dict:
         byts = batch * topk * bs * (256 + 4) + batch * H * 258
         res[name] = {"us": round(us, 2), "gbs": round(byts / us / 1e3, 1),
                      "frac_of_hbm": round(byts / us / 1e3 / PEAK_HBM_GBS, 4)}
+    return res
+
+
+def indexer_h16_config(L, steps: int) -> dict:
+    """The indexer at the reference wrapper's own precision (bf16 q and k,
+    examples/deepseek_v4/lightning_indexer.py:1250-1253) at config-5 size: 4096 tail
+    queries x 131072 keys, 64 heads x 128, causal, top-2048 (the full entry: the
+    16-bit MFMA logits kernel, then the streamed top-k; no group maxima).  The top-k
+    alone on the same logits is timed too; the indexer's share is the difference.
+    FLOP = 2 * 64 * 128 per visible pair, against the 2.5 PFLOP/s 16-bit MFMA peak."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream(dev).cuda_stream
+    S1, S2 = 4096, 131072
+    g = torch.Generator(device=dev).manual_seed(12)
+    q = torch.randn((1, S1, IDX_HEADS, IDX_DIM), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((1, S2, 1, IDX_DIM), generator=g, device=dev).to(torch.bfloat16)
+    w = torch.randn((1, S1, IDX_HEADS), generator=g, device=dev) / 8
+    idx = torch.empty((1, S1, 1, TOPK), dtype=torch.int32, device=dev)
+    wsb = L.dsa_lightning_indexer_varlen_workspace_bytes(S1, S2)
+    ws = torch.empty((wsb,), dtype=torch.uint8, device=dev)
+    logits = ws[: S1 * S2 * 4].view(torch.float32)
+    row_len = ws[(S1 * S2 * 4 + 255) // 256 * 256:][: S1 * 4].view(torch.int32)
+    idx2 = torch.empty((S1, TOPK), dtype=torch.int32, device=dev)
+
+    def full():
+        rc = L.dsa_lightning_indexer_h16_varlen(q.data_ptr(), k.data_ptr(), None, w.data_ptr(), None, 0, None, 0,
+                                                None, 0, 0, 0, 1, S1, S2, S1, IDX_HEADS, IDX_DIM, 0, TOPK, 3,
+                                                idx.data_ptr(), None, ws.data_ptr(), wsb, st)
+        if rc != 0:
+            raise RuntimeError(f"indexer_h16: {L.dsa_last_error().decode()}")
+
+    def tk():
+        rc = L.dsa_topk_f32(logits.data_ptr(), S1, S2, S2, row_len.data_ptr(), TOPK, 1, idx2.data_ptr(), None, st)
+        if rc != 0:
+            raise RuntimeError(f"topk of the h16 logits: {L.dsa_last_error().decode()}")
+
+    uf = _time_launches(full, max(2, steps // 2), warmup=3)
+    ut = _time_launches(tk, max(2, steps // 2))
+    fl = indexer_flops_causal(S1, S2)
+    ui = uf - ut
+    del q, k, w, idx, ws, logits, row_len, idx2
+    torch.cuda.empty_cache()
+    return {"dtype": "bf16", "indexer_topk_us": round(uf, 1), "topk_us": round(ut, 1),
+            "indexer_us_derived": round(ui, 1), "indexer_tflops": round(fl / ui / 1e6, 1),
+            "indexer_frac_of_bf16_peak": round(fl / ui / 1e6 / PEAK_BF16_TFLOPS, 4)}
+
+
+# bench_sfa decode shapes and the times the reference publishes for them on Ascend
+# (examples/sparse_flash_attention/bench_sfa/bench_sfa.py:106-153, README.md:31-34)
+SFA_SHAPES = ((2560, 109.76), (6400, 109.10), (48000, 108.98))
+
+
+def bench_sfa_configs(L, steps: int) -> dict:
+    """The reference's only published sparse-MLA decode shapes (bench_sfa.py:106-153):
+    T = 1 query, B = 1, 128 heads, D = 512 + 64 rope, top-2048 of the first
+    act_kv = 2560 keys (topk of uniform noise), 128-key pages with an identity block
+    table, scale 0.5, KV_S = 2560 / 6400 / 48000.  ``kernel_us``: dsa_sparse_mla_fwd
+    on a joined 576-wide page cache (HIP events, inputs resident); ``wrapper_us``:
+    dsa.sparse_attn_tilelang with separate rope tensors, which joins q and the key
+    cache per call as the reference wrapper does (sparse_flash_attn_pa_no_cv_pipeline.py:406).
+    ``ascend_tilelang_us``: the reference's published TileLang times (Ascend A2/A3)."""
+    import torch
+
+    import dsa
+
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream(dev).cuda_stream
+    res = {}
+    T, N, D, Dr, bs, act_kv, topk = 1, 128, 512, 64, 128, 2560, 2048
+    for kv_s, pub in SFA_SHAPES:
+        g = torch.Generator(device=dev).manual_seed(kv_s)
+        query = (torch.randn((T, N, D), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+        key = (torch.randn((kv_s // bs, bs, 1, D), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+        qr = (torch.randn((T, N, Dr), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+        kr = (torch.randn((kv_s // bs, bs, 1, Dr), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+        idx = torch.topk(torch.rand((T, 1, act_kv), generator=g, device=dev), topk, dim=-1).indices.int()
+        bt = torch.arange(kv_s // bs, dtype=torch.int32, device=dev).view(1, -1)
+        aq = torch.ones((1,), dtype=torch.int32, device=dev)
+        ak = torch.full((1,), act_kv, dtype=torch.int32, device=dev)
+        q576 = torch.cat((query, qr), -1).unsqueeze(0).contiguous()
+        kv576 = torch.cat((key, kr), -1).contiguous()
+        i4 = idx.view(1, T, 1, topk).contiguous()
+        qs = ak - aq
+        out = torch.empty((1, T, N, D), dtype=torch.bfloat16, device=dev)
+        lse = torch.empty((1, T, N), dtype=torch.float32, device=dev)
+        wsb = L.dsa_sparse_mla_workspace_bytes(1, T, N, topk, 0)
+        ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+
+        def kern():
+            rc = L.dsa_sparse_mla_fwd(q576.data_ptr(), kv576.data_ptr(), i4.data_ptr(), bt.data_ptr(), ak.data_ptr(),
+                                      qs.data_ptr(), None, 1, T, N, DQK, DV, kv576.shape[0] * bs, bs, bt.shape[1],
+                                      topk, 0.5, 1, 0, out.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws.numel(), st)
+            if rc != 0:
+                raise RuntimeError(f"bench_sfa: {L.dsa_last_error().decode()}")
+
+        def wrap():
+            dsa.sparse_attn_tilelang(query=query, key=key, value=key, sparse_indices=idx, scale_value=0.5,
+                                     sparse_block_size=1, actual_seq_lengths_query=aq, actual_seq_lengths_kv=ak,
+                                     query_rope=qr, key_rope=kr, layout_query="TND", layout_kv="PA_BSND",
+                                     sparse_mode=0, block_table=bt, attention_mode=2)
+
+        uk = _time_launches(kern, steps, warmup=3)
+        uw = _time_launches(wrap, steps, warmup=3)
+        byts = topk * DQK * 2 + N * DQK * 2 + topk * 4 + N * (DV * 2 + 4)
+        res[f"kv_s_{kv_s}"] = {"kernel_us": round(uk, 2), "wrapper_us": round(uw, 2),
+                               "ascend_tilelang_us": pub, "speedup_vs_ascend_kernel": round(pub / uk, 2),
+                               "algorithmic_bytes": byts}
+        del query, key, qr, kr, idx, q576, kv576, out, lse, ws
+    torch.cuda.empty_cache()
     return res
 
 
@@ -855,12 +968,17 @@ def main() -> int:
     f_idx = indexer_flops_causal(S1, S2)
     mla_tflops = f_mla / (per["mla"] * 1e-6) / 1e12
     idx_tflops = f_idx / (per["indexer"] * 1e-6) / 1e12
+    # the top-k's roofline reads every visible logit once; its group-maxima path
+    # reads only the groups the indexer's maxima admit, so its bandwidth is the
+    # profiled bytes over its time, and the full-row figure is a time ratio
     topk_bytes = 4.0 * sum(S2 - S1 + t + 1 for t in range(S1)) + 4.0 * S1 * TOPK
-    topk_gbs = topk_bytes / (per["topk"] * 1e-6) / 1e9
+    topk_roof_us = topk_bytes / PEAK_HBM_GBS / 1e3
+    topk_prof = read_profile(args.profile).get("topk", {})
+    topk_gbs = (topk_prof["hbm_bytes"] / (per["topk"] * 1e-6) / 1e9) if topk_prof.get("hbm_bytes") else None
 
     kern = {"indexer": ("mfma", idx_tflops, PEAK_FP8_TFLOPS, "TFLOP/s"),
             "mla": ("mfma", mla_tflops, PEAK_BF16_TFLOPS, "TFLOP/s"),
-            "topk": ("hbm", topk_gbs, PEAK_HBM_GBS, "GB/s")}
+            "topk": ("hbm", topk_gbs or 0.0, PEAK_HBM_GBS, "GB/s")}
     dom = max(kern, key=lambda k: per[k])
     bound, ach, peak, unit = kern[dom]
     prof = read_profile(args.profile).get(dom, {})
@@ -888,7 +1006,8 @@ def main() -> int:
         "indexer_topk_us": round(per["indexer"] + per["topk"], 2),
         "indexer_tflops": round(idx_tflops, 2),
         "indexer_frac_of_fp8_peak": round(idx_tflops / PEAK_FP8_TFLOPS, 4),
-        "topk_gbs": round(topk_gbs, 1),
+        "topk_gbs_measured": round(topk_gbs, 1) if topk_gbs else None,
+        "topk_full_row_roofline_us": round(topk_roof_us, 2),
         "mla_us": round(per["mla"], 2),
         "decode_us": {"indexer": round(per["dec_indexer"], 2), "topk": round(per["dec_topk"], 2),
                       "mla": round(per["dec_mla"], 2)},

@@ -13,6 +13,7 @@ import torch
 import dsa
 from dsa import inputs
 from oracle.dsa_oracle import indexer_scores, sparse_mla_fwd_gather, stable_topk
+from fullsize import check_mla_tokens, check_topk_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -101,6 +102,11 @@ def test_config4_prefill_full(gpu):
     _check_tokens(out, lse, inp["q"], inp["kv"], inp["indices"], tokens, inp["sm_scale"], 0)
     # every token's lse is finite (each row has at least its own position)
     assert torch.isfinite(lse).all()
+    # every token, on the first and last head of each wave, recomputed on the GPU
+    _say("config 4 every token")
+    kv0 = inp["kv"][0, :, 0]
+    check_mla_tokens(out[0], lse[0], inp["q"][0], lambda t0, t1, ii: kv0[ii], inp["indices"][0, :, 0],
+                     torch.arange(S, device=gpu), S, inp["sm_scale"], what="config 4")
 
 
 def test_config3_decode_full(gpu):
@@ -123,6 +129,15 @@ def test_config3_decode_full(gpu):
         ro, rl = sparse_mla_fwd_gather(d["q"][b:b + 1].cpu(), kvb, ar, d["sm_scale"], p_dtype=torch.bfloat16)
         torch.testing.assert_close(out[b:b + 1].float().cpu(), ro, **OUT_TOL)
         torch.testing.assert_close(lse[b:b + 1].cpu(), rl, **LSE_TOL)
+    # every sequence and every head, recomputed on the GPU through the page table
+    _say("config 3 every sequence")
+    bt = d["block_table"].long()
+
+    def gather(t0, t1, ii):
+        return d["kv"][bt[t0:t1].gather(1, ii // bs), ii % bs, 0]
+
+    check_mla_tokens(out[:, 0], lse[:, 0], d["q"][:, 0], gather, d["indices"][:, 0, 0], None,
+                     d["block_table"].shape[1] * bs, d["sm_scale"], heads=range(H), chunk=8, what="config 3")
 
 
 def _logit_rows_close(got, ref, what):
@@ -157,6 +172,9 @@ def test_config5_layer_chain(gpu):
         _logit_rows_close(got, ref, f"row {t}")
         ti, _ = stable_topk(got, TOPK)
         assert torch.equal(idx[0, t, 0].cpu(), ti[0]), f"top-k row {t}"
+    _say("config 5 top-k every row")
+    check_topk_rows(idx.view(S1, TOPK), logits.view(S1, S2), q_start + 1 + torch.arange(S1, device=gpu), TOPK,
+                    chunk=64, what="config 5 top-k")
     # the MLA over the chunk with the indexer's indices
     _say("config 5 sparse MLA over the chunk")
     g = torch.Generator(device=gpu).manual_seed(105)
@@ -165,6 +183,10 @@ def test_config5_layer_chain(gpu):
     out, lse = dsa.sparse_mla_fwd(q, kv, idx, DQK ** -0.5, q_start_index_s=q_start)
     torch.cuda.synchronize()
     _check_tokens(out, lse, q, kv, idx, [0, 5, 1024, 2047, 3333, 4095], DQK ** -0.5, q_start)
+    _say("config 5 sparse MLA every token")
+    kv0 = kv[0, :, 0]
+    check_mla_tokens(out[0], lse[0], q[0], lambda t0, t1, ii: kv0[ii], idx[0, :, 0],
+                     q_start + torch.arange(S1, device=gpu), S2, DQK ** -0.5, what="config 5 chunk")
     # decode step: 32 queries at position S2 over the same cache, as the benchmark
     # runs it (the 32 rows share the key cache: one batch row of 32 query rows
     # seeing every key), then the paged MLA (64-token pages, every sequence's
@@ -183,6 +205,7 @@ def test_config5_layer_chain(gpu):
         _logit_rows_close(got, ref, f"decode row {b}")
         ti, _ = stable_topk(got, TOPK)
         assert torch.equal(didx[b, 0, 0].cpu(), ti[0]), f"decode top-k row {b}"
+    check_topk_rows(didx.view(B, TOPK), dlog.view(B, S2), None, TOPK, what="config 5 decode top-k")
     pool = kv.view(S2 // bs, bs, 1, DQK)
     bt = torch.arange(S2 // bs, dtype=torch.int32, device=gpu).repeat(B, 1).contiguous()
     mq = (torch.randn((B, 1, H, DQK), generator=g, device=gpu) * 0.5).to(torch.bfloat16)
@@ -194,3 +217,6 @@ def test_config5_layer_chain(gpu):
                                        p_dtype=torch.bfloat16)
         torch.testing.assert_close(dout[b:b + 1].float().cpu(), ro, **OUT_TOL)
         torch.testing.assert_close(dlse[b:b + 1].cpu(), rl, **LSE_TOL)
+    kvd = kv[0, :, 0]
+    check_mla_tokens(dout[:, 0], dlse[:, 0], mq[:, 0], lambda t0, t1, ii: kvd[ii], didx[:, 0, 0], None, S2,
+                     DQK ** -0.5, heads=range(H), chunk=8, what="config 5 decode")

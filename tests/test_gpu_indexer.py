@@ -14,6 +14,7 @@ import dsa
 from dsa import inputs
 from oracle.dsa_oracle import lightning_indexer as ref_indexer
 from oracle.dsa_oracle import stable_topk
+from fullsize import check_topk_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -112,6 +113,32 @@ def test_config2_rows_sample(gpu):
         _logit_close(logits[0, t, :L].cpu(), ref)
         ti, _ = stable_topk(logits[0, t, :L].cpu().unsqueeze(0), 2048)
         assert torch.equal(idx[0, t, 0].cpu(), ti[0])
+    # every row's top-k against the stable sort of the same logits, on the GPU
+    lens = 32768 - 4096 + 1 + torch.arange(4096, device=gpu)
+    check_topk_rows(idx.view(4096, 2048), logits.view(4096, 32768), lens, 2048, what="config 2 top-k")
+
+
+@pytest.mark.parametrize("K,mode", [(4096, 3), (8192, 3), (8192, 0)])
+def test_sparse_count_above_2048_long_rows(gpu, K, mode):
+    # sparse_count multiples of 1024 up to 8192 (lightning_indexer.py:1240-1241) at
+    # 131072 keys: more than 2K / 16 groups reach the threshold, so the rows take
+    # the streamed top-k instead of the group-maxima path; every row's indices
+    # against the stable sort of the same logits, and sampled logits against the oracle
+    S1, S2 = 64, 131072
+    print(f"indexer sparse_count={K} mode={mode} S1={S1} S2={S2}", flush=True)
+    inp = inputs.indexer_fp8(B=1, S1=S1, S2=S2, seed=K + mode, device=gpu)
+    idx, _, logits = dsa.lightning_indexer(inp["q"], inp["k"], inp["w"], key_scale=inp["key_scale"],
+                                           sparse_count=K, sparse_mode=mode, return_logits=True)
+    torch.cuda.synchronize()
+    assert tuple(idx.shape) == (1, S1, 1, K)
+    lens = (S2 - S1 + 1 + torch.arange(S1, device=gpu)) if mode == 3 else None
+    check_topk_rows(idx.view(S1, K), logits.view(S1, S2), lens, K, what=f"sparse_count {K}")
+    kdq = inp["k"][0, :, 0].float().cpu() * inp["key_scale"][0].cpu().unsqueeze(1)
+    for t in (0, S1 - 1):
+        L = S2 - S1 + t + 1 if mode == 3 else S2
+        qk = torch.relu(inp["q"][0, t].float().cpu() @ kdq[:L].T)
+        ref = (inp["w"][0, t].cpu().unsqueeze(1) * qk).sum(0)
+        _logit_close(logits[0, t, :L].cpu(), ref)
 
 
 def _ragged_fp8(seed, lens_q, lens_k, D=128, H=64):

@@ -147,18 +147,22 @@ def test_reference_factory_fp16_sentinel_convention(gpu):
 def test_reference_factory_kv_stride(gpu, S, sk, kv_stride, topk):
     # compressed KV rows (kv_stride > 1): the golden's causal rule over compressed
     # positions, q_start = sk * kv_stride - S, and key 0 kept for the first
-    # kv_stride - 1 rows (example_sparse_flash_attn.py:255-292); every list holds
-    # key 0 and future keys, padded with the sentinel sk
+    # kv_stride - 1 rows, listed or not (example_sparse_flash_attn.py:255-292);
+    # lists hold future keys, padded with the sentinel sk; row 0's list omits key 0
+    # (and is full when sk > topk), the other rows list it
     g = torch.Generator().manual_seed(100 + S + kv_stride)
     q = torch.randn((1, S, 128, 576), generator=g).to(torch.bfloat16)
     kv = torch.randn((1, sk, 1, 576), generator=g).to(torch.bfloat16)
     idx = torch.full((1, S, 1, topk), sk, dtype=torch.int32)
     n = min(topk, sk)
     for t in range(S):
-        perm = torch.randperm(sk, generator=g)[:n]
-        if not (perm == 0).any():
-            perm[0] = 0
-        idx[0, t, 0, :n] = perm.to(torch.int32)
+        if t == 0:
+            perm = (torch.randperm(sk - 1, generator=g) + 1)[:n]
+        else:
+            perm = torch.randperm(sk, generator=g)[:n]
+            if not (perm == 0).any():
+                perm[0] = 0
+        idx[0, t, 0, :perm.numel()] = perm.to(torch.int32)
     print(f"factory kv_stride={kv_stride} S={S} sk={sk}", flush=True)
     kern = dsa.sparse_attention_fwd(heads=128, dim=512, tail_dim=64, topk=topk, kv_stride=kv_stride)
     out = kern(q.to(gpu), kv.to(gpu), idx.to(gpu)).float().cpu()
@@ -221,6 +225,10 @@ def test_sparse_attn_tilelang_signature(gpu, rope, T, act_q):
     qr = (torch.randn((T, N, Dr), generator=g) * 0.5).bfloat16() if rope else None
     kr = (torch.randn((KV_S // bs, bs, 1, Dr), generator=g) * 0.5).bfloat16() if rope else None
     idx = torch.topk(torch.rand((T, 1, act_kv), generator=g), topk, dim=-1).indices.int()
+    # padded rows past act_q hold NaN / Inf (as an uninitialised buffer may): their
+    # output rows must still come back as zeros
+    query[act_q:, :, 0] = float("nan")
+    query[act_q:, :, 1] = float("inf")
     bt = torch.arange(KV_S // bs, dtype=torch.int32).view(1, -1)
     aq, ak = torch.tensor([act_q], dtype=torch.int32), torch.tensor([act_kv], dtype=torch.int32)
     print(f"sparse_attn_tilelang rope={rope} T={T} act_q={act_q}", flush=True)
@@ -237,7 +245,7 @@ def test_sparse_attn_tilelang_signature(gpu, rope, T, act_q):
     ro, _ = sparse_mla_fwd_gather(q[:act_q].unsqueeze(0), kv, idx[:act_q].unsqueeze(0), 0.5, block_table=bt,
                                   q_start_index_s=act_kv - act_q, is_causal=True, p_dtype=torch.bfloat16)
     torch.testing.assert_close(out[:act_q].float().cpu(), ro[0], **OUT_TOL)
-    assert not out[act_q:].any()
+    assert torch.equal(out[act_q:].float().cpu(), torch.zeros_like(out[act_q:].float().cpu()))
 
 
 @pytest.mark.parametrize("H,splits", [(128, 1), (128, 4), (64, 2), (16, 1)])

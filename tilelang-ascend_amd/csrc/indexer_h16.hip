@@ -6,9 +6,13 @@
 //
 // with the rows, causal rule, layouts (BSND / TND query rows; BSND / TND / paged
 // keys), row lengths and -inf convention of the fp8 kernel (indexer.hip) and of
-// the golden cpu_lightning_indexer (:199-335): q.k is accumulated in fp32 from the
-// exact 16-bit products, so the logits follow the golden's fp32 arithmetic up to
-// the order of the additions.  N1 <= 64 heads (the missing heads count as zero).
+// the golden cpu_lightning_indexer (:199-335).  q.k is accumulated in fp32 from
+// the exact 16-bit products, as the golden computes it, but the head sum is formed
+// as (sum_h w_h d_h + sum_h w_h |d_h|) / 2 rather than sum_h w_h ReLU(d_h): the
+// negative heads' terms cancel between the two sums, so a logit's rounding error
+// is bounded by a few fp32 ulps of sum_h |w_h d_h| (not of the logit itself), and
+// a logit much smaller than that sum carries a larger relative error than the
+// golden's own rounding.  N1 <= 64 heads (the missing heads count as zero).
 //
 // Work decomposition.  One workgroup = 8 waves = 8 query tokens (one per wave, two
 // waves per SIMD) of one batch row x one chunk of keys.  A wave holds its token's

@@ -466,9 +466,10 @@ def sparse_attention_fwd(heads: int, dim: int, tail_dim: int, topk: int, kv_stri
     position ``Skv * kv_stride - S + m``) sees it when that position is at least
     ``n * kv_stride + kv_stride - 1``, the causal rule of the golden
     ``ref_sparse_attention_fwd_interface`` (:255-280); its first ``kv_stride - 1``
-    rows also keep a listed key 0 (:280; a row whose list lacks key 0 is not
-    given one).  Indices that fail the rule are set to -1 on the device before
-    the launch."""
+    rows always attend key 0, listed or not (:280: the golden sets that mask entry
+    after the causal AND).  Indices that fail the rule are set to -1 on the device
+    before the launch, and those rows get key 0 in one extra list column when
+    their list lacks it."""
     def _pow2(x):
         return x > 0 and (x & (x - 1)) == 0
     assert _pow2(dim), f"haven't check padding correctness yet, dim={dim}"
@@ -491,6 +492,13 @@ def sparse_attention_fwd(heads: int, dim: int, tail_dim: int, topk: int, kv_stri
         last = torch.div(skv * kv_stride - S + m + 1, kv_stride, rounding_mode="floor") - 1
         last = torch.where(m < kv_stride - 1, last.clamp_min(0), last).view(1, S, 1, 1)
         idx = torch.where(indices.to(torch.int64) <= last, indices, torch.full_like(indices, -1)).to(torch.int32)
+        # rows m < kv_stride - 1 see key 0 whatever their list holds: append it
+        # (once) where the filtered list lacks it
+        nrow = min(kv_stride - 1, S)
+        extra = torch.full((*idx.shape[:3], 1), -1, dtype=torch.int32, device=idx.device)
+        has0 = (idx[:, :nrow] == 0).any(dim=-1, keepdim=True)
+        extra[:, :nrow] = torch.where(has0, -1, 0).to(torch.int32)
+        idx = torch.cat((idx, extra), dim=-1)
         return sparse_mla_fwd(q, kv, idx.contiguous(), scale, is_causal=False, return_lse=False)
 
     return kernel
@@ -545,7 +553,8 @@ def sparse_attn_tilelang(query: torch.Tensor, key: torch.Tensor, value: torch.Te
     idx = sparse_indices.to(device=dev, dtype=torch.int32).contiguous().view(1, T, 1, -1)
     out = sparse_mla_fwd(q, kv, idx, float(scale_value), block_table=block_table, seq_len_kv=act_kv,
                          q_start_index_s=act_kv - act_q, is_causal=True, return_lse=False)[0]
-    out.mul_((torch.arange(T, device=dev, dtype=torch.int32) < act_q).view(T, 1, 1))
+    # masked_fill, not a multiply: a padded row may hold NaN / Inf, and NaN * 0 is NaN
+    out.masked_fill_((torch.arange(T, device=dev, dtype=torch.int32) >= act_q).view(T, 1, 1), 0)
     return out
 
 
