@@ -154,3 +154,28 @@ def test_group_max_overflow_and_loose_bounds(gpu):
     torch.cuda.synchronize()
     ri, rv = stable_topk(x, 2048)
     _assert_exact(gi.cpu(), gv.cpu(), ri, rv)
+
+
+def test_decode_shape_rows(gpu):
+    # the decode step's top-k: 32 rows x 131072 logits with group maxima; random
+    # rows, ties (values on a 1/8 and a 1/2 grid), short and masked rows, a row of
+    # mostly equal values (its group list overflows) and a block of equal maxima,
+    # all bit-exact against the stable sort
+    R, N, K = 32, 131072, 2048
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn((R, N), generator=g)
+    x[1] = torch.round(x[1] * 8) / 8
+    x[2, 70000:] = float("-inf")
+    x[3, :] = 0.25
+    x[3, ::997] = 1.0
+    x[4, 5000:6000] = 3.0
+    x[5] = torch.round(x[5] * 2) / 2
+    row_len = torch.full((R,), N, dtype=torch.int32)
+    row_len[6] = 40000
+    row_len[7] = 2 * 16 * K + 3
+    gm = _group_max(x, row_len)
+    print("topk decode shape 32 x 131072", flush=True)
+    gi, gv = dsa.topk_selector(x.to(gpu), K, row_len=row_len.to(gpu), group_max=gm.to(gpu), return_values=True)
+    torch.cuda.synchronize()
+    ri, rv = stable_topk(x, K, row_len=row_len)
+    _assert_exact(gi.cpu(), gv.cpu(), ri, rv)
