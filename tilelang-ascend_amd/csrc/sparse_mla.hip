@@ -1352,12 +1352,18 @@ int launch_mla(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
 
 int choose_splits(int64_t tokens, int nhg, int topk) {
   // split the index list until the 256 CUs are covered, keeping >= 256 keys per
-  // split (more splits cost more fp32 partials than the extra CUs return); a
-  // handful of rows (single-token decode) is latency bound instead, and splits
-  // down to 128 keys (below that the combine costs more than it saves)
-  const int min_keys = tokens * nhg >= 16 ? 256 : 128;
+  // split (more splits cost more partials than the extra CUs return).  A handful
+  // of rows (single-token decode) is latency bound instead: each halving saves
+  // key steps down to splits of 64 keys (two steps; beyond that the combine's
+  // extra rounds cost more), but the first split, which adds the combine launch,
+  // pays only for lists of more than 128 keys.  Single-token decode, one
+  // MI355X: top-2048 16 -> 32 splits 29.6 -> 27.9 us, V4 csa 4 -> 8 splits
+  // 21.3 -> 18.9 us, a 128-key list 1 -> 2 splits 15.8 -> 16.1 us.
+  const bool few = tokens * nhg < 16;
+  const int min_keys = few ? 64 : 256;
   int ns = 1;
-  while (tokens * nhg * ns < 256 && (topk + 2 * ns - 1) / (2 * ns) >= min_keys) ns *= 2;
+  if (!few || topk > 128)
+    while (tokens * nhg * ns < 256 && (topk + 2 * ns - 1) / (2 * ns) >= min_keys) ns *= 2;
   while ((topk + ns - 1) / ns > kMaxKeysPerSplit) ++ns;
   return ns;
 }
