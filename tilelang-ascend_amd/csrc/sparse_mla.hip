@@ -1233,10 +1233,11 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
 // block.  The lse, scale and slice of kCombineU splits are all loaded before any
 // is used, so a row costs one round trip per kCombineU splits; chunks beyond the
 // first are merged online (the running sums rescaled to the new maximum).
-constexpr int kCombineU = 8;
+// kCombineU is 4 for up to 4 splits (no idle load slots: config-3 decode 59.6 ->
+// 58.0 us, bit-identical), else 8 (16 or 32 measured no faster at 32 splits).
 constexpr int kCombineRows = 4;  // rows per 256-thread block
 
-template <bool F16>
+template <bool F16, int kCombineU>
 __global__ __launch_bounds__(256) void mla_combine_kernel(const uint16_t* __restrict__ part_o,
                                                           const float* __restrict__ part_lse,
                                                           const float* __restrict__ part_scale,
@@ -1458,12 +1459,17 @@ int sparse_mla_run(const MlaRun& r, const char* what) {
   if (rc != kOk || ns == 1) return rc;
   const int64_t rows = T * r.H;
   const dim3 cgrid((unsigned)((rows + kCombineRows - 1) / kCombineRows));
-  if (r.f16)
-    hipLaunchKernelGGL(mla_combine_kernel<true>, cgrid, dim3(256), 0, st, p.part_o, p.part_lse, p.part_scale, rows, r.H,
-                       ns, p.out, r.lse);
-  else
-    hipLaunchKernelGGL(mla_combine_kernel<false>, cgrid, dim3(256), 0, st, p.part_o, p.part_lse, p.part_scale, rows,
-                       r.H, ns, p.out, r.lse);
+  auto combine = [&](auto U) {
+    constexpr int u = decltype(U)::value;
+    if (r.f16)
+      hipLaunchKernelGGL((mla_combine_kernel<true, u>), cgrid, dim3(256), 0, st, p.part_o, p.part_lse, p.part_scale,
+                         rows, r.H, ns, p.out, r.lse);
+    else
+      hipLaunchKernelGGL((mla_combine_kernel<false, u>), cgrid, dim3(256), 0, st, p.part_o, p.part_lse, p.part_scale,
+                         rows, r.H, ns, p.out, r.lse);
+  };
+  if (ns <= 4) combine(IntC<4>{});
+  else combine(IntC<8>{});
   return check_launch("dsa_sparse_mla_fwd(combine)");
 }
 
