@@ -87,6 +87,16 @@ def test_paged_decode_small(gpu):
     _check(inp, gpu, block_table=inp["block_table"], seq_len_kv=inp["seq_len_kv"], is_causal=False)
 
 
+@pytest.mark.parametrize("B,topk", [(1, 2048), (1, 640), (1, 192), (1, 128), (3, 2048), (15, 1024), (8, 96)])
+def test_latency_bound_decode_splits(gpu, B, topk):
+    # a handful of decode rows takes the automatic split count of a latency-bound
+    # launch (down to 64-key splits; a list of <= 128 keys unsplit): every row
+    # against the oracle, including lists that end in -1 padding
+    inp = inputs.mla_decode(B=B, ctx=8192, H=128, topk=topk, block_size=64, seed=40 + B + topk)
+    inp["indices"][0, 0, 0, topk - topk // 5:] = -1
+    _check(inp, gpu, block_table=inp["block_table"], seq_len_kv=inp["seq_len_kv"], is_causal=False)
+
+
 def test_d512_with_sink(gpu):
     inp = inputs.mla_prefill(B=1, S=16, Skv=256, H=64, topk=128, seed=15, d_qk=512)
     g = torch.Generator().manual_seed(1)
