@@ -20,18 +20,22 @@
 // Work decomposition.  One workgroup = 16 waves = 16 query tokens (one per wave)
 // of one batch row x one chunk of keys.  A wave holds its token's A operands
 // (64 heads x 128 dims of fp8 plus the u pieces) in registers.  K streams through
-// a 4-stage LDS ring of 64-key tiles filled with global_load_lds (three tiles in
-// flight while one is computed); a tile stores 16-byte chunk j of key s at slot
-// j ^ (s & 7) ^ ((s >> 3) & 1), which keeps the B-operand reads (16 keys x one
-// chunk, 128-byte rows) on distinct banks for both 8- and 16-lane LDS phases.  Per 16-key block
-// a wave issues 4 fp8 MFMAs (v_mfma_scale_f32_16x16x128_f8f6f4) and 16 FMAs, and
-// once per tile the u MFMA for one block of its group of 4 waves (the results
-// pass through LDS).  The 4 lane groups then exchange their partial sums with
-// permlane swaps (a reduce-scatter) so that lane l ends up with key 64-tile + l
-// and the tile is one coalesced 256-byte store.  That epilogue of tile i runs in
-// iteration i+1, behind the first MFMAs of tile i+1, so the waves released by a
-// barrier start with matrix work rather than all doing VALU work at once.  Workgroups that share a key chunk are placed
-// on the same XCD so the chunk stays in that XCD's L2.
+// an 8-stage LDS ring of 64-key tiles filled with global_load_lds, consumed in
+// pairs of tiles with one workgroup barrier per pair (four tiles in flight while
+// a pair is computed; one barrier per tile cost ~2 % more at 128K keys); a tile
+// stores 16-byte chunk j of key s at slot j ^ (s & 7) ^ ((s >> 3) & 1), which
+// keeps the B-operand reads (16 keys x one chunk, 128-byte rows) on distinct
+// banks for both 8- and 16-lane LDS phases.  Per 16-key block a wave issues 4 fp8
+// MFMAs (v_mfma_scale_f32_16x16x128_f8f6f4) and 16 FMAs, and once per tile the u
+// MFMA for one block of its group of 4 waves (the results pass through LDS).  The
+// 4 lane groups then exchange their partial sums with permlane swaps (a
+// reduce-scatter) so that lane l ends up with key 64-tile + l and the tile is one
+// coalesced 256-byte store.  That reduce-scatter of tile i runs in tile i+1 and
+// the rest of its epilogue (u.k, scale, store) in tile i+2, behind the barrier
+// that publishes tile i's u.k and behind the first MFMAs of the tile, so the
+// waves released by a barrier start with matrix work rather than all doing VALU
+// work at once.  Workgroups that share a key chunk are placed on the same XCD so
+// the chunk stays in that XCD's L2.
 #include "dsa_common.h"
 
 namespace {
@@ -42,7 +46,7 @@ constexpr int kTokPerBlock = kWaves;  // one query token per wave
 constexpr int kHeads = 64;
 constexpr int kDim = 128;
 constexpr int kKeyTile = 64;
-constexpr int kStages = 4;
+constexpr int kStages = 8;  // ring of key tiles; one barrier per pair of tiles
 constexpr int kTileBytes = kKeyTile * kDim;      // 8 KB
 constexpr int kKeyLoaders = kTileBytes / 1024;   // waves 0..7 load 1 KB of keys each
 constexpr int kScaleLoader = kKeyLoaders;        // wave 8 loads the tile's key scales
@@ -176,7 +180,12 @@ __device__ __forceinline__ void wait_vmcnt_upto(int n) {
     case 2: dsa::wait_vmcnt<2>(); break;
     case 3: dsa::wait_vmcnt<3>(); break;
     case 4: dsa::wait_vmcnt<4>(); break;
-    default: dsa::wait_vmcnt<5>(); break;
+    case 5: dsa::wait_vmcnt<5>(); break;
+    case 6: dsa::wait_vmcnt<6>(); break;
+    case 7: dsa::wait_vmcnt<7>(); break;
+    case 8: dsa::wait_vmcnt<8>(); break;
+    case 9: dsa::wait_vmcnt<9>(); break;
+    default: dsa::wait_vmcnt<10>(); break;
   }
 }
 
@@ -215,7 +224,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   __shared__ __align__(16) uint8_t usplit[kWaves][kSplits][kDim + 16];
   __shared__ int uexp[kWaves];
   __shared__ __align__(16) float wsh[kWaves][kHeads];  // each token's weights
-  __shared__ __align__(16) float lin[2][kWaves][kKeyTile];  // u.k per token and key, two tiles
+  __shared__ __align__(16) float lin[4][kWaves][kKeyTile];  // u.k per token and key, four tiles
 
   // XCD-aware mapping: the work items (key group (b, chunk), token block), key
   // group major, are cut into 8 equal contiguous ranges, one per XCD (workgroup
@@ -326,7 +335,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   // first, below).
   if constexpr (!PAGED) {
 #pragma unroll
-    for (int i = 0; i < kStages - 1; ++i) issue(i);
+    for (int i = 0; i < kStages - 2; ++i) issue(i);
   }
   // q: lane (g, c) holds head 16*mt + c, bytes [32g, 32g+32) of the head.
   dsa::i32x8 qa[4];
@@ -416,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   if constexpr (PAGED) {
     dsa::wait_vmcnt<0>();
 #pragma unroll
-    for (int i = 0; i < kStages - 1; ++i) issue(i);
+    for (int i = 0; i < kStages - 2; ++i) issue(i);
   }
 
   // u.k hand-off: this wave writes block ublk of its group's 4 tokens, reads its own token.
@@ -428,8 +437,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   // times the key scale, masked, stored.  tile < 0 issues a store that the
   // buffer range check drops, so every iteration has exactly one store.
   // lk: this lane's u.k of the tile (read from LDS by the caller, already waited for).
-  auto finish = [&](const float (&ap)[4], float ksp, float lk, int tile, auto SLOT) {
-    constexpr int kSlot = decltype(SLOT)::value;  // tile % 4, or -1: the last tile (run-time slot)
+  auto reduce = [&](const float (&ap)[4]) {
     float r02, r13;
     {
       const auto s0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ap[0]), __float_as_uint(ap[2]), false, false);
@@ -438,7 +446,10 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
       r13 = __uint_as_float(s1[0]) + __uint_as_float(s1[1]);
     }
     const auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(r02), __float_as_uint(r13), false, false);
-    float sum = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
+    return __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
+  };
+  auto finish = [&](float sum, float ksp, float lk, int tile, auto SLOT) {
+    constexpr int kSlot = decltype(SLOT)::value;  // tile % 4, or -1: the last tiles (run-time slot)
     int voff = 0x40000000;  // beyond any descriptor range: dropped
     if (tile >= 0) {
       sum += lk;
@@ -480,32 +491,40 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   };
 
   const dsa::f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  // ap / ksp: partial sums and key scale of the previous tile; s2 / k2: the
+  // reduced sums and key scale of the tile before it
   float ap[4] = {0.f, 0.f, 0.f, 0.f};
-  float ksp = 1.f;
+  float ksp = 1.f, s2 = 0.f, k2 = 1.f;
   // One tile; ST = it % kStages is a compile-time ring slot, so every LDS offset
-  // below is an instruction immediate.
+  // below is an instruction immediate.  Tiles go in pairs (it even, it + 1) with
+  // one barrier per pair; a tile's epilogue runs two tiles later, in the next
+  // pair, behind the barrier that publishes its u.k.
   auto step = [&](int it, auto STC) {
     constexpr int ST = decltype(STC)::value;
+    constexpr int SUB = ST & 1;
     constexpr uint32_t so = ST * kTileBytes;
-    // This wave's load of tile `it` is done once at most min(2 + it, 5) newer
-    // memory operations are in flight (the loads of the next two tiles, one logit
-    // store per finished tile; a group-maxima store every fourth tile only adds
-    // to them, so the bound stays safe); its LDS writes and reads of the previous
-    // iteration are complete.
-    if (loader) wait_vmcnt_upto(min(kStages - 2 + it, 2 * kStages - 3));
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ksp));
-    __builtin_amdgcn_s_barrier();
-    // The four waves of a SIMD are served oldest-first; a wave lowers its priority
-    // as it gets through the tile, so the four finish the tile together instead
-    // of the oldest idling at the next barrier while the youngest runs alone.
-    __builtin_amdgcn_s_setprio(3);
-    issue(it + kStages - 1);
+    if constexpr (SUB == 0) {
+      // This wave's loads of tiles it and it + 1 are done once at most
+      // min(4 + it, 10) newer memory operations are in flight (the loads of the
+      // next four tiles, one logit store per finished tile; a group-maxima store
+      // every fourth tile only adds to them, so the bound stays safe); its LDS
+      // writes and reads of the previous pair are complete.
+      if (loader) wait_vmcnt_upto(min(kStages - 4 + it, 10));
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ksp), "+v"(k2));
+      __builtin_amdgcn_s_barrier();
+      // The four waves of a SIMD are served oldest-first; a wave lowers its
+      // priority as it gets through the pair, so the four finish it together
+      // instead of the oldest idling at the next barrier.
+      __builtin_amdgcn_s_setprio(3);
+      issue(it + kStages - 2);
+      issue(it + kStages - 1);
+    }
 
     float ksc = 1.f;
     if (sbase != nullptr) ksc = lds_read_f32<ST * kKeyTile * 4>(sc_addr);
-    // u.k of the previous tile (written before the barrier); issued ahead of the
-    // B fragments so that their first wait covers it
-    float lkp = lds_read_f32<((ST + 1) & 1) * kLinBuf>(lin_rd);
+    // u.k of tile it - 2 (written in the previous pair); issued ahead of the B
+    // fragments so that their first wait covers it
+    float lkp = lds_read_f32<((ST + 2) & 3) * kLinBuf>(lin_rd);
     float a[4];
     // B fragments of block blk (16 keys x 128 B); the next block's read is in
     // flight while the current block's MFMAs run.
@@ -528,23 +547,29 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)  // D[row = head 16mt + 4g + i][col = key 16blk + c]
         d[mt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[mt], bf, zero, 0, 0, 0, 127, 0, 127);
-      if constexpr (blk == 0) finish(ap, ksp, lkp, it - 1, dsa::IntC<(ST + 3) & 3>{});
+      if constexpr (blk == 0) {
+        const float s1 = reduce(ap);  // tile it - 1
+        finish(s2, k2, lkp, it - 2, dsa::IntC<(ST + 2) & 3>{});
+        s2 = s1;
+        k2 = ksp;
+      }
       float acc = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc = fmaf(wh[mt][i], fabsf(d[mt][i]), acc);
       a[blk] = acc;
-      __builtin_amdgcn_s_setprio(blk < 2 ? 2 - blk : 0);
+      constexpr int prio = 3 - ((4 * SUB + blk + 1) * 3) / 8;
+      __builtin_amdgcn_s_setprio(prio);
     });
     {
-      // u.k of block ublk for the group's 4 tokens -> LDS (read in the next iteration).
+      // u.k of block ublk for the group's 4 tokens -> LDS (read two tiles later).
       dsa::i32x4 k0v = dsa::lds_read_b128<so>(ub_rd0), k1v = dsa::lds_read_b128<so>(ub_rd1);
       lds_wait2<0>(k0v, k1v);
       const dsa::i32x8 ub = {k0v[0], k0v[1], k0v[2], k0v[3], k1v[0], k1v[1], k1v[2], k1v[3]};
       const dsa::f32x4 du = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ua, ub, zero, 0, 0, 0, uscale, 0, 127);
       const float lv = (du[0] + du[1]) + (du[2] + du[3]);
-      asm volatile("ds_write_b32 %0, %1 offset:%2" : : "v"(lin_wr), "v"(lv), "i"((ST & 1) * kLinBuf) : "memory");
+      asm volatile("ds_write_b32 %0, %1 offset:%2" : : "v"(lin_wr), "v"(lv), "i"((ST & 3) * kLinBuf) : "memory");
     }
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) ap[blk] = a[blk];
@@ -555,16 +580,28 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
     if (it + 1 < ntiles) step(it + 1, dsa::IntC<1>{});
     if (it + 2 < ntiles) step(it + 2, dsa::IntC<2>{});
     if (it + 3 < ntiles) step(it + 3, dsa::IntC<3>{});
+    if (it + 4 < ntiles) step(it + 4, dsa::IntC<4>{});
+    if (it + 5 < ntiles) step(it + 5, dsa::IntC<5>{});
+    if (it + 6 < ntiles) step(it + 6, dsa::IntC<6>{});
+    if (it + 7 < ntiles) step(it + 7, dsa::IntC<7>{});
   }
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ksp));
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ksp), "+v"(k2));
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_s_setprio(0);
-  {
-    const int last = ntiles - 1;
-    float lk = (last & 1) ? lds_read_f32<kLinBuf>(lin_rd) : lds_read_f32<0>(lin_rd);
+  // the epilogues of the last two tiles
+  auto lin_of = [&](int t) {
+    float lk;
+    switch (t & 3) {
+      case 0: lk = lds_read_f32<0>(lin_rd); break;
+      case 1: lk = lds_read_f32<kLinBuf>(lin_rd); break;
+      case 2: lk = lds_read_f32<2 * kLinBuf>(lin_rd); break;
+      default: lk = lds_read_f32<3 * kLinBuf>(lin_rd); break;
+    }
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lk));
-    finish(ap, ksp, lk, last, dsa::IntC<-1>{});
-  }
+    return lk;
+  };
+  if (ntiles >= 2) finish(s2, k2, lin_of(ntiles - 2), ntiles - 2, dsa::IntC<-1>{});
+  finish(reduce(ap), ksp, lin_of(ntiles - 1), ntiles - 1, dsa::IntC<-1>{});
   // No LDS DMA may still be in flight when the workgroup's LDS is released.
   if (loader) dsa::wait_vmcnt<0>();
 }
