@@ -48,8 +48,7 @@ constexpr int kDim = 128;
 constexpr int kKeyTile = 64;
 constexpr int kStages = 8;  // ring of key tiles; one barrier per pair of tiles
 constexpr int kTileBytes = kKeyTile * kDim;      // 8 KB
-constexpr int kKeyLoaders = kTileBytes / 1024;   // waves 0..7 load 1 KB of keys each
-constexpr int kScaleLoader = kKeyLoaders;        // wave 8 loads the tile's key scales
+constexpr int kKeyLoaders = kTileBytes / 1024;   // 1 KB loads per tile (waves 0..7 or 8..15)
 constexpr int kSplits = 4;                       // fp8 pieces of u
 constexpr int kE4m3Max = 448;
 constexpr int kMaxChunk = 32768;                 // keys per workgroup at most
@@ -284,24 +283,49 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   const int ntiles = (k1 - k0 + kKeyTile - 1) / kKeyTile;
   const uint8_t* kbase = PAGED ? p.k : p.k + kbase_row * kDim;
   const float* sbase = p.key_scale ? (PAGED ? p.key_scale : p.key_scale + kbase_row) : nullptr;
-  const bool loader = wave < kKeyLoaders || (wave == kScaleLoader && sbase != nullptr);
-  // Loader lane l of wave w fills LDS bytes [w KB + 16 l, +16) of a tile: key
-  // s = 8w + l/8, slot l%8, which holds the key's chunk (l%8) ^ swz(s).
-  const int lkey = 8 * wave + (lane >> 3);
+  // The ring is filled a pair of tiles at a time, and every wave issues exactly
+  // one 1 KB load per pair: waves 0-7 fill the pair's first tile, waves 8-15 its
+  // second, so the loads' address work does not make some waves late at the
+  // pair barrier.  Lane l of wave w fills LDS bytes [(w % 8) KB + 16 l, +16) of
+  // its tile: key s = 8 (w % 8) + l/8, slot l%8, which holds the key's chunk
+  // (l%8) ^ swz(s).  Waves 7 and 15 also load their tile's 64 key scales.
+  const int lslice = wave & 7, lhalf = wave >> 3;
+  const int lkey = 8 * lslice + (lane >> 3);
   const int lchunk = (lane & 7) ^ (lkey & 7) ^ ((lkey >> 3) & 1);
-  auto issue = [=](int tile) {
-    const int t = tile < ntiles ? tile : ntiles - 1;  // past the end: reload the last tile (never read)
+  const bool scale_loader = lslice == kKeyLoaders - 1 && sbase != nullptr;
+  // Contiguous keys are read through buffer descriptors over the batch row's
+  // keys [0, k1): 16-byte records for the keys (record 8 s + chunk), 4-byte
+  // records for the scales.  A key at or past k1 (the tail of the last tile, or
+  // a tile past the end, issued so that every pair has its one load) reads
+  // zeros, and no lane computes a 64-bit address.
+  const __amdgpu_buffer_rsrc_t krsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)16, PAGED ? 0 : k1 * (kDim / 16), 0x00020000);
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(sbase != nullptr ? sbase : g_zero_scale), (short)4, PAGED || sbase == nullptr ? 0 : k1, 0x00020000);
+  const uint32_t krec = (uint32_t)(lkey * (kDim / 16) + lchunk);
+  // the loads of the pair (tile0, tile0 + 1); tile0 is even
+  auto issue = [=](int tile0) {
+    const int t = tile0 + lhalf;
     const int kt0 = k0 + t * kKeyTile;
-    if (wave < kKeyLoaders) {
-      const int key = min(kt0 + lkey, k1 - 1);
-      const int row = PAGED ? krows[key - k0] : key;
+    DSA_LDS void* kdst = (DSA_LDS void*)&ktile[t & (kStages - 1)][1024 * lslice];
+    DSA_LDS void* sdst = (DSA_LDS void*)&kscale[t & (kStages - 1)][0];
+    if constexpr (PAGED) {
+      // past the end: the last tile's keys again, into a free ring slot (never read)
+      const int tt = t < ntiles ? t : ntiles - 1;
+      const int key = min(k0 + tt * kKeyTile + lkey, k1 - 1);
+      const int row = krows[key - k0];
       const uint8_t* src = row >= 0 ? kbase + (int64_t)row * kDim + 16 * lchunk : g_zero_key + 16 * lchunk;
-      __builtin_amdgcn_global_load_lds(src, (DSA_LDS void*)&ktile[t & (kStages - 1)][1024 * wave], 16, 0, 0);
-    } else if (wave == kScaleLoader && sbase != nullptr) {
-      const int key = min(kt0 + lane, k1 - 1);
-      const int row = PAGED ? krows[key - k0] : key;
-      const float* src = row >= 0 ? sbase + row : g_zero_scale + lane;
-      __builtin_amdgcn_global_load_lds(src, (DSA_LDS void*)&kscale[t & (kStages - 1)][0], 4, 0, 0);
+      __builtin_amdgcn_global_load_lds(src, kdst, 16, 0, 0);
+      if (scale_loader) {
+        const int skey = min(k0 + tt * kKeyTile + lane, k1 - 1);
+        const int srow = krows[skey - k0];
+        const float* ssrc = srow >= 0 ? sbase + srow : g_zero_scale + lane;
+        __builtin_amdgcn_global_load_lds(ssrc, sdst, 4, 0, 0);
+      }
+    } else {
+      __builtin_amdgcn_struct_ptr_buffer_load_lds(krsrc, kdst, 16, (uint32_t)kt0 * (kDim / 16) + krec, 0, 0, 0, 0);
+      if (scale_loader)
+        __builtin_amdgcn_struct_ptr_buffer_load_lds(srsrc, sdst, 4, (uint32_t)(kt0 + lane), 0, 0, 0, 0);
     }
   };
   // ---- per-token operands -------------------------------------------------
@@ -335,7 +359,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   // first, below).
   if constexpr (!PAGED) {
 #pragma unroll
-    for (int i = 0; i < kStages - 2; ++i) issue(i);
+    for (int i = 0; i < kStages - 2; i += 2) issue(i);
   }
   // q: lane (g, c) holds head 16*mt + c, bytes [32g, 32g+32) of the head.
   dsa::i32x8 qa[4];
@@ -425,7 +449,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   if constexpr (PAGED) {
     dsa::wait_vmcnt<0>();
 #pragma unroll
-    for (int i = 0; i < kStages - 2; ++i) issue(i);
+    for (int i = 0; i < kStages - 2; i += 2) issue(i);
   }
 
   // u.k hand-off: this wave writes block ublk of its group's 4 tokens, reads its own token.
@@ -504,12 +528,14 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
     constexpr int SUB = ST & 1;
     constexpr uint32_t so = ST * kTileBytes;
     if constexpr (SUB == 0) {
-      // This wave's loads of tiles it and it + 1 are done once at most
-      // min(4 + it, 10) newer memory operations are in flight (the loads of the
-      // next four tiles, one logit store per finished tile; a group-maxima store
-      // every fourth tile only adds to them, so the bound stays safe); its LDS
-      // writes and reads of the previous pair are complete.
-      if (loader) wait_vmcnt_upto(min(kStages - 4 + it, 10));
+      // This wave's load for the pair (it, it + 1) is done once at most
+      // min(2 + it, 8) newer memory operations are in flight: it was issued at
+      // pair it - 6 (or in the prologue, followed by the prologue's later
+      // loads), and each pair since issued one load and one logit store per
+      // tile; a group-maxima store every fourth tile, or a scale load (waves 7
+      // and 15, after their key load), only adds to them, so the bound stays
+      // safe.  Its LDS writes and reads of the previous pair are complete.
+      wait_vmcnt_upto(min(2 + it, 8));
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ksp), "+v"(k2));
       __builtin_amdgcn_s_barrier();
       // The four waves of a SIMD are served oldest-first; a wave lowers its
@@ -517,7 +543,6 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
       // instead of the oldest idling at the next barrier.
       __builtin_amdgcn_s_setprio(3);
       issue(it + kStages - 2);
-      issue(it + kStages - 1);
     }
 
     float ksc = 1.f;
@@ -603,7 +628,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   if (ntiles >= 2) finish(s2, k2, lin_of(ntiles - 2), ntiles - 2, dsa::IntC<-1>{});
   finish(reduce(ap), ksp, lin_of(ntiles - 1), ntiles - 1, dsa::IntC<-1>{});
   // No LDS DMA may still be in flight when the workgroup's LDS is released.
-  if (loader) dsa::wait_vmcnt<0>();
+  dsa::wait_vmcnt<0>();
 }
 
 // ---- decode form: batch rows of at most kDecMaxTok query tokens ---------------
