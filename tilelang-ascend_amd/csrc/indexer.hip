@@ -212,8 +212,9 @@ __device__ float g_zero_scale[kKeyTile];
 
 // PAGED: keys live in a page pool [blocks * block_size, D] addressed through
 // p.block_table; the physical rows of this workgroup's key chunk are resolved
-// once into LDS.
-template <bool PAGED>
+// once into LDS.  GMAX: the maxima of 16-key groups are emitted (p.gmax); as a
+// template parameter it costs the loop nothing when they are not wanted.
+template <bool PAGED, bool GMAX>
 __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) {
   __shared__ __align__(1024) uint8_t ktile[kStages][kTileBytes];
   __shared__ int32_t krows[PAGED ? kMaxChunkPaged : 1];
@@ -400,6 +401,8 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
       r1 = fmaf(-sig, __builtin_amdgcn_cvt_f32_fp8(pk, 1), r1);
     }
   }
+  // without key scales the scale ring holds 1.0 for good (no scale loads are issued)
+  if (sbase == nullptr && tid < kStages * kKeyTile) (&kscale[0][0])[tid] = 1.f;
   __syncthreads();
   // u pieces of the group's 4 tokens as A rows: row 4*tq + sp = piece sp of token
   // grp0 + tq; lane (g, c) holds row c, bytes 32g..32g+31.  In the result, lane
@@ -423,7 +426,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   const __amdgpu_buffer_rsrc_t ost = __builtin_amdgcn_make_buffer_rsrc(
       orow, (short)0, tok_ok ? (kend - k0) * 4 : 0, 0x00020000);
   // Group maxima: one float per 16 keys (the chunk start is a multiple of 64).
-  const bool want_gmax = p.gmax != nullptr;
+  constexpr bool want_gmax = GMAX;
   // Group maxima of four consecutive tiles are gathered in one register (lane
   // 16 j + s holds group j of tile 4 b + s) and stored together.
   const int gslot_lane = lane & 15;
@@ -474,19 +477,18 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
   };
   auto finish = [&](float sum, float ksp, float lk, int tile, auto SLOT) {
     constexpr int kSlot = decltype(SLOT)::value;  // tile % 4, or -1: the last tiles (run-time slot)
-    int voff = 0x40000000;  // beyond any descriptor range: dropped
-    if (tile >= 0) {
-      sum += lk;
-      if (k0 + (tile + 1) * kKeyTile <= L) {  // the whole tile is visible (wave-uniform)
-        sum *= ksp;
-      } else {
-        const int key = k0 + tile * kKeyTile + lane;
-        sum = key < L ? sum * ksp : -__builtin_inff();
-      }
-      voff = (tile * kKeyTile + lane) * 4;
+    // A tile < 0 (the first pair has no finished tile) has a negative offset,
+    // which the descriptor's range check drops as a huge unsigned one.
+    sum += lk;
+    if (k0 + (tile + 1) * kKeyTile <= L) {  // the whole tile is visible (wave-uniform)
+      sum *= ksp;
+    } else {
+      const int key = k0 + tile * kKeyTile + lane;
+      sum = key < L ? sum * ksp : -__builtin_inff();
     }
+    const int voff = (tile * kKeyTile + lane) * 4;
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sum), ost, voff, 0, 0);
-    if (want_gmax) {
+    if constexpr (want_gmax) {
       // max over each row of 16 lanes (16 consecutive keys): v_max_f32 with DPP
       // quad swaps, then half-row and row mirrors (each DPP source written two
       // wait states earlier).  v_max_f32 returns the non-NaN operand, and the
@@ -545,8 +547,7 @@ __global__ __launch_bounds__(kThreads) void indexer_fp8_kernel(IndexerParams p) 
       issue(it + kStages - 2);
     }
 
-    float ksc = 1.f;
-    if (sbase != nullptr) ksc = lds_read_f32<ST * kKeyTile * 4>(sc_addr);
+    const float ksc = lds_read_f32<ST * kKeyTile * 4>(sc_addr);
     // u.k of tile it - 2 (written in the previous pair); issued ahead of the B
     // fragments so that their first wait covers it
     float lkp = lds_read_f32<((ST + 2) & 3) * kLinBuf>(lin_rd);
@@ -923,10 +924,14 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
   const int64_t nblocks = p.per_xcd * kNumXcd;
   if (nblocks <= 0) return kOk;
   if (nblocks > 0x7fffffff) return set_error(kUnsupported, "indexer: grid too large");
-  if (block_table != nullptr)
-    hipLaunchKernelGGL(indexer_fp8_kernel<true>, dim3((unsigned)nblocks), dim3(kThreads), 0, stream, p);
-  else
-    hipLaunchKernelGGL(indexer_fp8_kernel<false>, dim3((unsigned)nblocks), dim3(kThreads), 0, stream, p);
+  const dim3 grid((unsigned)nblocks), block(kThreads);
+  if (block_table != nullptr) {
+    if (p.gmax != nullptr) hipLaunchKernelGGL((indexer_fp8_kernel<true, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((indexer_fp8_kernel<true, false>), grid, block, 0, stream, p);
+  } else {
+    if (p.gmax != nullptr) hipLaunchKernelGGL((indexer_fp8_kernel<false, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((indexer_fp8_kernel<false, false>), grid, block, 0, stream, p);
+  }
   return check_launch("dsa_indexer_logits_fp8");
 }
 
