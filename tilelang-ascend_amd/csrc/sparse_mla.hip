@@ -72,6 +72,7 @@ struct MlaParams {
   int block_size, max_blocks;
   int nsplit, keys_per_split, nhg;
   int balance;                  // token order balanced for short causal rows (balanced_token)
+  int order;                    // the 4-wave form gathers each list's rows in row-range order (order_rows)
   uint32_t buf_records;         // 16-byte records of the KV pool (buffer-addressed gathers of the 4-wave form)
   float scale_log2;
   int causal;
@@ -108,7 +109,10 @@ __device__ __align__(16) uint16_t g_zero_row[576];
 // DeepSeek-V4 key-set generation.  All NT threads of the workgroup take part.
 // Returns the largest j this thread wrote with a valid row (-1: none), so that
 // the caller can stop after the last valid key instead of stepping through the
-// -1 padding of a short list.
+// -1 padding of a short list.  rmin / rmax take the smallest and largest key
+// this thread wrote with a valid row (unchanged when it wrote none): the list's
+// index for contiguous and paged lists, the row otherwise; with lidx (not null)
+// those two kinds also write each entry's index to lidx[j].
 // mid() runs once the list's own loads (indices, lengths, page table) are issued,
 // so loads it issues (the query operands) overlap the resolution without
 // delaying it: memory results retire in issue order, so a query load issued
@@ -116,10 +120,21 @@ __device__ __align__(16) uint16_t g_zero_row[576];
 struct NoMid {
   __device__ void operator()() const {}
 };
-template <int NT, typename Mid = NoMid>
+// Kinds of index list.  A kernel compiled for one kind has no branch join between
+// the kinds' row resolutions: at such a join the compiler waited for every load
+// in flight, the query operands included, before the first gathers could issue.
+constexpr int kListAny = 0;     // decided at run time (DeepSeek-V4 key sets, resolved rows, paged, contiguous)
+constexpr int kListContig = 1;  // indices into one contiguous KV sequence per batch row
+constexpr int kListPaged = 2;   // indices through a block table into a page pool
+template <int NT, int KIND = kListAny, typename Mid = NoMid>
 __device__ __forceinline__ int resolve_rows(const MlaParams& p, int64_t token, int b, int s, int kbeg, int nkeys,
-                                             int32_t* rows, int tid, Mid mid = Mid{}) {
-  if (p.v4_on) {
+                                             int32_t* rows, int tid, Mid mid, int& rmin, int& rmax,
+                                             int32_t* lidx = nullptr) {
+  auto seen = [&](int32_t row) {
+    rmin = min(rmin, (int)row);
+    rmax = max(rmax, (int)row);
+  };
+  if (KIND == kListAny && p.v4_on) {
     mid();
     __shared__ int v4_sh[2];  // batch of this row, first -1 of its compressed list
     if (tid == 0) {
@@ -137,8 +152,12 @@ __device__ __forceinline__ int resolve_rows(const MlaParams& p, int64_t token, i
     const int stop = v4_sh[1];
     int last = -1;
     for (int j = tid; j < nkeys; j += NT) {
-      rows[j] = vb >= 0 ? dsa::v4_row(p.v4, token, vb, kbeg + j, stop) : -1;
-      if (rows[j] >= 0) last = j;
+      const int32_t row = vb >= 0 ? dsa::v4_row(p.v4, token, vb, kbeg + j, stop) : -1;
+      rows[j] = row;
+      if (row >= 0) {
+        last = j;
+        seen(row);
+      }
     }
     return last;
   } else {
@@ -160,7 +179,7 @@ __device__ __forceinline__ int resolve_rows(const MlaParams& p, int64_t token, i
     // the compiler may not hoist mid()'s loads above the list's loads
     asm volatile("" ::: "memory");
     int last = -1;
-    if (p.direct) {
+    if (KIND == kListAny && p.direct) {
       mid();
       // resolved rows: bit 30 selects the second pool
 #pragma unroll
@@ -169,7 +188,10 @@ __device__ __forceinline__ int resolve_rows(const MlaParams& p, int64_t token, i
         const int rr = idx[r] & ~dsa::kRowTag2;
         const bool ok = idx[r] >= 0 && (int64_t)rr < ((idx[r] & dsa::kRowTag2) ? p.pool_rows2 : p.pool_rows);
         if (j < nkeys) rows[j] = ok ? idx[r] : -1;
-        if (j < nkeys && ok) last = j;
+        if (j < nkeys && ok) {
+          last = j;
+          seen(idx[r]);
+        }
       }
       return last;
     }
@@ -179,7 +201,7 @@ __device__ __forceinline__ int resolve_rows(const MlaParams& p, int64_t token, i
       ok[r] = idx[r] >= 0 && idx[r] < kvl && (int64_t)idx[r] < p.skv;
       if (p.causal) ok[r] = ok[r] && idx[r] <= qs + s;
     }
-    if (p.block_table) {
+    if (KIND == kListPaged || (KIND == kListAny && p.block_table)) {
       // table entries at clamped positions (max_blocks > 0), loaded without a
       // branch per load, ahead of mid()'s loads; their values are taken only
       // after mid() (a wait for them is not hoisted above its loads)
@@ -199,7 +221,11 @@ __device__ __forceinline__ int resolve_rows(const MlaParams& p, int64_t token, i
         const int64_t rr = (int64_t)page[r] * p.block_size + idx[r] % p.block_size;
         const bool okr = page[r] >= 0 && rr < p.pool_rows;
         if (j < nkeys) rows[j] = okr ? (int32_t)rr : -1;
-        if (j < nkeys && okr) last = j;
+        if (lidx != nullptr && j < nkeys) lidx[j] = idx[r];
+        if (j < nkeys && okr) {
+          last = j;
+          seen(idx[r]);
+        }
       }
     } else {
       mid();
@@ -207,11 +233,104 @@ __device__ __forceinline__ int resolve_rows(const MlaParams& p, int64_t token, i
       for (int r = 0; r < R; ++r) {
         const int j = tid + r * NT;
         if (j < nkeys) rows[j] = ok[r] ? (int32_t)((int64_t)b * p.skv + idx[r]) : -1;
-        if (j < nkeys && ok[r]) last = j;
+        if (lidx != nullptr && j < nkeys) lidx[j] = idx[r];
+        if (j < nkeys && ok[r]) {
+          last = j;
+          seen(idx[r]);
+        }
       }
     }
     return last;
   }
+}
+
+// Reorders the valid rows of rows[0, nlist) by 64 buckets of their list index
+// lidx[j], bucket (lidx[j] - lo) >> sh with sh the smallest shift that maps
+// hi - lo below 64, keeping list order within a bucket, and drops the invalid
+// (-1) rows; returns the number of valid rows, which then fill rows[0, n).
+// Neighbouring tokens of a prefill on one XCD, whose lists are gathered step by
+// step in parallel, then sweep the sequence in the same direction at the same
+// pace, so the rows they share are fetched once into that XCD's L2 and DRAM
+// pages are read in order; the sums are taken in another order, which changes
+// only their rounding.  The order is a function of the list alone (ballot
+// ranks, no atomics; the same for a contiguous and a paged copy of the
+// sequence), so results are reproducible.  tab: 2304 ints of free LDS.  All NT
+// threads take part.
+template <int NT>
+__device__ __forceinline__ int order_rows(int32_t* rows, const int32_t* lidx, int nlist, int lo, int hi,
+                                          int32_t* tab, int tid) {
+  constexpr int R = kMaxKeysPerSplit / NT;  // list entries per thread: j = tid + r NT
+  constexpr int NW = NT / 64;
+  constexpr int NB = 64;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int span = hi - lo;
+  const int sh = max(0, (32 - __builtin_clz((uint32_t)span | 1u)) - 6);  // span >> sh < 64
+  // phase 1: group g = r NW + wave (list entries 256 r + 64 wave .. + 63, so group
+  // order is list order): each entry's rank among the group's entries of its
+  // bucket (a ballot match on the bucket's 7 bits) and each bucket's count in
+  // tab[g][bucket].  One wave's LDS writes land in issue order, so its zeros
+  // precede its counts without a barrier.
+  int32_t v[R];
+  uint32_t key[R];  // bucket (NB: invalid) | rank << 8
+#pragma unroll
+  for (int r = 0; r < R; ++r) tab[(r * NW + wave) * NB + lane] = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int j = tid + r * NT;
+    v[r] = j < nlist ? rows[j] : -1;
+    const int bk = v[r] >= 0 ? (lidx[j] - lo) >> sh : NB;
+    uint64_t m = ~0ull;
+#pragma unroll
+    for (int k = 0; k < 7; ++k) {
+      const uint64_t bal = __ballot((bk >> k) & 1);
+      m &= ((bk >> k) & 1) ? bal : ~bal;
+    }
+    const int rank = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    if (rank == 0 && bk < NB) tab[(r * NW + wave) * NB + bk] = __popcll(m);
+    key[r] = (uint32_t)bk | ((uint32_t)rank << 8);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  // phase 2: lane b of wave w sums bucket b over groups R w .. R w + R - 1, then
+  // the offsets of every (group, bucket): the bucket's start (an exclusive scan
+  // over buckets, one bucket per lane) + the counts of earlier groups
+  int c[R], run = 0;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    c[i] = run;
+    run += tab[(wave * R + i) * NB + lane];
+  }
+  int32_t* const part = tab + R * NW * NB;  // [NW][NB]
+  part[wave * NB + lane] = run;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  int pre = 0, tot = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < NW; ++w2) {
+    const int t = part[w2 * NB + lane];
+    tot += t;
+    pre += w2 < wave ? t : 0;
+  }
+  int inc = tot;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(inc, d);
+    inc += lane >= d ? t : 0;
+  }
+  const int nvalid = __shfl(inc, 63);
+#pragma unroll
+  for (int i = 0; i < R; ++i) tab[(wave * R + i) * NB + lane] = inc - tot + pre + c[i];
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  // phase 3: every valid row to its place
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int bk = (int)(key[r] & 0xffu);
+    if (bk < NB) rows[tab[(r * NW + wave) * NB + bk] + (int)(key[r] >> 8)] = v[r];
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  return nvalid;
 }
 
 // Token of workgroup (xcd, rq) when p.balance is set (one sequence, one split, one
@@ -308,7 +427,8 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
 
   // ---- resolve this split's indices to physical rows (-1 = skip); the list
   // ends after its last valid key (steps past it would add exactly nothing) ----
-  int last_ok = resolve_rows<NT>(p, token, b, s, kbeg, nlist, rows, tid);
+  int rmin = 0x7fffffff, rmax = -1;  // (unused here)
+  int last_ok = resolve_rows<NT, kListAny>(p, token, b, s, kbeg, nlist, rows, tid, NoMid{}, rmin, rmax);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) last_ok = max(last_ok, __shfl_xor(last_ok, o));
   int32_t* const last_slot = rows + p.keys_per_split;  // one per wave
@@ -734,7 +854,7 @@ __device__ __forceinline__ int32_t lds_read_b32(uint32_t addr) {
 // record index per lane; an index past the pool reads zeros), which issues in about
 // a fifth of the time of a 64-bit per-lane address.  The hardware forms the byte
 // offset in 32 bits, so this is for pools of at most 4 GiB with rows from one pool.
-template <int DQK, bool F16, bool BUF>
+template <int DQK, bool F16, bool BUF, int KIND>
 __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   constexpr int NT = 256;
   constexpr int KS = DQK / 16;          // score k-steps: 36 (576) or 32 (512)
@@ -788,23 +908,47 @@ __global__ __launch_bounds__(256, 1) void mla_w4_kernel(MlaParams p) {
   // fetch overlaps the row resolution and the first gathers; the first score
   // MFMA waits for it together with the gathers of step 0.
   dsa::i32x4 qf[KS];
-  int last_ok = resolve_rows<NT>(p, token, b, s, kbeg, nlist, rows, tid, [&]() {
-    const uint16_t* qp = p.q + (token * p.H + (head_ok ? head : 0)) * DQK + 8 * hh;
+  // with p.order the list's indices go to the (empty) ring for order_rows
+  int32_t* const lidx = reinterpret_cast<int32_t*>(smem + 16384);
+  int rmin = 0x7fffffff, rmax = -1;
+  int last_ok = resolve_rows<NT, KIND>(
+      p, token, b, s, kbeg, nlist, rows, tid,
+      [&]() {
+        const uint16_t* qp = p.q + (token * p.H + (head_ok ? head : 0)) * DQK + 8 * hh;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const dsa::i32x4*>(qp + 16 * ks);
-  });
+        for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const dsa::i32x4*>(qp + 16 * ks);
+      },
+      rmin, rmax, p.order ? lidx : nullptr);
   // (a lane past the last head computes with head 0's query; its column of S, P
   // and O is never written out, and no other head's column depends on it)
   // The list ends after its last valid key: the steps past it (the -1 padding of
   // a short causal row) would add exactly nothing.
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) last_ok = max(last_ok, __shfl_xor(last_ok, o));
-  int32_t* const last_slot = rows + p.keys_per_split;  // one per wave
-  if (lane == 0) last_slot[wave] = last_ok;
+  for (int o = 32; o > 0; o >>= 1) {
+    last_ok = max(last_ok, __shfl_xor(last_ok, o));
+    rmin = min(rmin, __shfl_xor(rmin, o));
+    rmax = max(rmax, __shfl_xor(rmax, o));
+  }
+  // one slot per wave: its last valid key, then its smallest and largest row
+  int32_t* const last_slot = rows + p.keys_per_split;
+  if (lane == 0) {
+    last_slot[wave] = last_ok;
+    last_slot[4 + wave] = rmin;
+    last_slot[8 + wave] = rmax;
+  }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // rows[] and last_slot[] written
   __builtin_amdgcn_s_barrier();                        // ... by every wave
-  const int nkeys = __builtin_amdgcn_readfirstlane(
+  int nkeys = __builtin_amdgcn_readfirstlane(
       max(max(last_slot[0], last_slot[1]), max(last_slot[2], last_slot[3])) + 1);
+  if (p.order && nkeys > 0) {
+    const int lo = min(min(last_slot[4], last_slot[5]), min(last_slot[6], last_slot[7]));
+    const int hi = max(max(last_slot[8], last_slot[9]), max(last_slot[10], last_slot[11]));
+    // the (empty) ring holds the ordering's tables
+    static_assert(16384 + 4 * kMaxKeysPerSplit <= STAGE, "tables and indices fit the first ring stage");
+    nkeys = __builtin_amdgcn_readfirstlane(order_rows<NT>(rows, lidx, nlist, __builtin_amdgcn_readfirstlane(lo),
+                                                          __builtin_amdgcn_readfirstlane(hi),
+                                                          reinterpret_cast<int32_t*>(smem), tid));
+  }
 
   // ---- gathers: wave w fills chunk pairs w, w + 4, .. of every step; lane l of a
   // block load writes 16-byte slot l of the block, i.e. key gk = (l / 2) ^ 4 (w % 2),
@@ -1307,11 +1451,11 @@ int launch_mla_stages(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
   return dsa::check_launch("dsa_sparse_mla_fwd");
 }
 
-template <int DQK, bool F16, bool BUF>
+template <int DQK, bool F16, bool BUF, int KIND>
 int launch_mla_w4_as(const MlaParams& p, int64_t nblocks, hipStream_t stream) {
-  // ring, the rows[] list, one last-valid-key slot per wave
-  const size_t smem = (size_t)kW4Stages * kKT * DQK * 2 + sizeof(int32_t) * ((size_t)p.keys_per_split + 4);
-  auto fn = mla_w4_kernel<DQK, F16, BUF>;
+  // ring, the rows[] list, one last-valid-key slot and a row range per wave
+  const size_t smem = (size_t)kW4Stages * kKT * DQK * 2 + sizeof(int32_t) * ((size_t)p.keys_per_split + 12);
+  auto fn = mla_w4_kernel<DQK, F16, BUF, KIND>;
   static std::atomic<int> lds_reserved[dsa::kMaxDevices];
   const int rc = dsa::reserve_lds((const void*)fn, smem, lds_reserved, "sparse_mla");
   if (rc != dsa::kOk) return rc;
@@ -1333,10 +1477,16 @@ int launch_mla_w4(MlaParams p, int64_t nblocks, hipStream_t stream) {
   const int64_t records = rows * (DQK / 8);
   if (p.kv2 == nullptr && records * 16 <= ((int64_t)1 << 32)) {
     p.buf_records = (uint32_t)records;
-    return launch_mla_w4_as<DQK, F16, true>(p, nblocks, stream);
+    // the bf16, d_qk 576 path of DeepSeek's layers has kernels per list kind
+    if constexpr (DQK == 576 && !F16) {
+      if (!p.v4_on && !p.direct)
+        return p.block_table ? launch_mla_w4_as<DQK, F16, true, kListPaged>(p, nblocks, stream)
+                             : launch_mla_w4_as<DQK, F16, true, kListContig>(p, nblocks, stream);
+    }
+    return launch_mla_w4_as<DQK, F16, true, kListAny>(p, nblocks, stream);
   }
   p.buf_records = 0u;
-  return launch_mla_w4_as<DQK, F16, false>(p, nblocks, stream);
+  return launch_mla_w4_as<DQK, F16, false, kListAny>(p, nblocks, stream);
 }
 
 // Workgroup form.  More than 64 heads: the 4-wave, 128-head form (one
@@ -1427,6 +1577,9 @@ int sparse_mla_run(const MlaRun& r, const char* what) {
   p.scale_log2 = r.sm_scale * kLog2e;
   p.causal = r.is_causal;
   p.balance = 0;
+  // index order of the gathers where neighbouring query tokens of a sequence
+  // share rows (a prefill, contiguous or paged)
+  p.order = r.S > 1 && !r.direct && r.v4 == nullptr;
 
   p.nhg = (r.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
   int ns = r.num_splits > 0 ? r.num_splits : choose_splits(T, p.nhg, r.topk);
