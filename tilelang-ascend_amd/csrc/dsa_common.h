@@ -137,6 +137,20 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave, VALU only: DPP row shifts
+// by 1, 2, 4, 8 scan each row of 16 lanes, then row broadcasts of lanes 15 and
+// 31 carry the row totals into the rows above (lanes of masked rows add 0).
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t x) {
+  int v = (int)x;
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
+  return (uint32_t)v;
+}
+
 // Cross-lane reductions over the lane groups l ^ 16 and l ^ 32 (gfx950 permlane swaps).
 __device__ __forceinline__ float xor16_max(float x) {
   auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);

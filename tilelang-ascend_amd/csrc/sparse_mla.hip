@@ -279,14 +279,19 @@ __device__ __forceinline__ int order_rows(int32_t* rows, const int32_t* lidx, in
     const int j = tid + r * NT;
     v[r] = j < nlist ? rows[j] : -1;
     const int bk = v[r] >= 0 ? (lidx[j] - lo) >> sh : NB;
-    uint64_t m = ~0ull;
+    // lanes whose bucket agrees with this lane's in every bit: per bit, the
+    // ballot of the bit, inverted (flip = ~0) where this lane's bit is 0
+    uint32_t mlo = ~0u, mhi = ~0u;
 #pragma unroll
     for (int k = 0; k < 7; ++k) {
-      const uint64_t bal = __ballot((bk >> k) & 1);
-      m &= ((bk >> k) & 1) ? bal : ~bal;
+      const uint32_t bit = ((uint32_t)bk >> k) & 1u;
+      const uint64_t bal = __ballot(bit);
+      const uint32_t flip = bit - 1u;
+      mlo &= (uint32_t)bal ^ flip;
+      mhi &= (uint32_t)(bal >> 32) ^ flip;
     }
-    const int rank = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-    if (rank == 0 && bk < NB) tab[(r * NW + wave) * NB + bk] = __popcll(m);
+    const int rank = (int)__builtin_amdgcn_mbcnt_hi(mhi, __builtin_amdgcn_mbcnt_lo(mlo, 0u));
+    if (rank == 0 && bk < NB) tab[(r * NW + wave) * NB + bk] = __popc(mlo) + __popc(mhi);
     key[r] = (uint32_t)bk | ((uint32_t)rank << 8);
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -311,13 +316,8 @@ __device__ __forceinline__ int order_rows(int32_t* rows, const int32_t* lidx, in
     tot += t;
     pre += w2 < wave ? t : 0;
   }
-  int inc = tot;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int t = __shfl_up(inc, d);
-    inc += lane >= d ? t : 0;
-  }
-  const int nvalid = __shfl(inc, 63);
+  const int inc = (int)dsa::wave_inclusive_scan((uint32_t)tot);
+  const int nvalid = __builtin_amdgcn_readlane(inc, 63);
 #pragma unroll
   for (int i = 0; i < R; ++i) tab[(wave * R + i) * NB + lane] = inc - tot + pre + c[i];
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");

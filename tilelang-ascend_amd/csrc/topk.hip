@@ -78,24 +78,10 @@ struct Shared {
   uint32_t flag;
 };
 
-// Inclusive prefix sum over the 64 lanes of a wave, VALU only: DPP row shifts
-// by 1, 2, 4, 8 scan each row of 16 lanes, then row broadcasts of lanes 15 and
-// 31 carry the row totals into the rows above (lanes of masked rows add 0).
-__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t x) {
-  int v = (int)x;
-  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
-  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
-  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
-  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
-  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
-  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
-  return (uint32_t)v;
-}
-
 // Exclusive prefix sum over the 1024 threads of the block.
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wsum) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const uint32_t x = wave_inclusive_scan(v);
+  const uint32_t x = dsa::wave_inclusive_scan(v);
   if (lane == 63) wsum[wid] = x;
   __syncthreads();
   uint32_t pre = 0;
