@@ -186,8 +186,10 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
       krows[i] = (pg >= 0 && row < p.pool_rows) ? (int32_t)row : -1;
     }
   }
+  // without key scales the scale ring holds 1.0 for good (no scale loads are issued)
+  if (p.key_scale == nullptr && tid < kHStages * kHTile) (&kscale[0][0])[tid] = 1.f;
   dsa::wait_vmcnt<0>();  // operands in registers before the ring's loads are counted
-  __syncthreads();       // krows[] ready
+  __syncthreads();       // krows[] (and the scale ring) ready
 
   // ---- key tiles: wave w's load i fills 1 KB block 2 w + i of the tile: lane l
   // loads key 4 (2 w + i) + l / 16, 16-byte slot l % 16 holding chunk
@@ -196,26 +198,49 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
   const uint16_t* kbase = PAGED ? p.k : p.k + kbase_row * kHDim;
   const float* sbase = p.key_scale ? (PAGED ? p.key_scale : p.key_scale + kbase_row) : nullptr;
   const int nload = kHLoadsPerTile + ((wave == 0 && sbase != nullptr) ? 1 : 0);
+  // Contiguous keys are read through buffer descriptors over the batch row's
+  // keys [0, k1): 16-byte records for the keys (record 16 s + chunk), 4-byte
+  // records for the scales; a key at or past k1 (the tail of the last tile, or a
+  // tile past the end, issued so that the ring's counts hold) reads zeros, and
+  // no lane computes a 64-bit address.
+  const __amdgpu_buffer_rsrc_t krsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)16, PAGED ? 0 : k1 * (kHDim / 8), 0x00020000);
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(sbase != nullptr ? sbase : g_zero_scale16), (short)4, PAGED || sbase == nullptr ? 0 : k1, 0x00020000);
   auto issue = [&](int tile) {
-    const int t = tile < ntiles ? tile : ntiles - 1;  // past the end: reload the last tile (never read)
-    const int kt0 = k0 + t * kHTile;
     unsigned char* dst = &ktile[tile % kHStages][0];
+    if constexpr (PAGED) {
+      const int t = tile < ntiles ? tile : ntiles - 1;  // past the end: the last tile again (never read)
+      const int kt0 = k0 + t * kHTile;
 #pragma unroll
-    for (int i = 0; i < kHLoadsPerTile; ++i) {
-      const int kk = 4 * (kHLoadsPerTile * wave + i) + (lane >> 4);
-      const int key = min(kt0 + kk, k1 - 1);
-      const int row = PAGED ? krows[key - k0] : key;
-      const int c = (lane & 15) ^ (kk & 15);
-      const uint16_t* src = row >= 0 ? kbase + (int64_t)row * kHDim + 8 * c : g_zero_key16 + 8 * c;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
-                                       (DSA_LDS void*)(dst + 1024 * (kHLoadsPerTile * wave + i)), 16, 0, 0);
-    }
-    if (wave == 0 && sbase != nullptr) {
-      const int key = min(kt0 + lane, k1 - 1);
-      const int row = PAGED ? krows[key - k0] : key;
-      const float* src = row >= 0 ? sbase + row : g_zero_scale16 + lane;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (DSA_LDS void*)&kscale[tile % kHStages][0], 4,
-                                       0, 0);
+      for (int i = 0; i < kHLoadsPerTile; ++i) {
+        const int kk = 4 * (kHLoadsPerTile * wave + i) + (lane >> 4);
+        const int key = min(kt0 + kk, k1 - 1);
+        const int row = krows[key - k0];
+        const int c = (lane & 15) ^ (kk & 15);
+        const uint16_t* src = row >= 0 ? kbase + (int64_t)row * kHDim + 8 * c : g_zero_key16 + 8 * c;
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                         (DSA_LDS void*)(dst + 1024 * (kHLoadsPerTile * wave + i)), 16, 0, 0);
+      }
+      if (wave == 0 && sbase != nullptr) {
+        const int key = min(kt0 + lane, k1 - 1);
+        const int row = krows[key - k0];
+        const float* src = row >= 0 ? sbase + row : g_zero_scale16 + lane;
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (DSA_LDS void*)&kscale[tile % kHStages][0],
+                                         4, 0, 0);
+      }
+    } else {
+      const uint32_t kt0 = (uint32_t)(k0 + tile * kHTile);
+#pragma unroll
+      for (int i = 0; i < kHLoadsPerTile; ++i) {
+        const int kk = 4 * (kHLoadsPerTile * wave + i) + (lane >> 4);
+        const uint32_t rec = (uint32_t)(kk * (kHDim / 8) + ((lane & 15) ^ (kk & 15)));
+        __builtin_amdgcn_struct_ptr_buffer_load_lds(krsrc, (DSA_LDS void*)(dst + 1024 * (kHLoadsPerTile * wave + i)),
+                                                    16, kt0 * (kHDim / 8) + rec, 0, 0, 0, 0);
+      }
+      if (wave == 0 && sbase != nullptr)
+        __builtin_amdgcn_struct_ptr_buffer_load_lds(srsrc, (DSA_LDS void*)&kscale[tile % kHStages][0], 4,
+                                                    kt0 + (uint32_t)lane, 0, 0, 0, 0);
     }
   };
 
@@ -273,12 +298,9 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
       }
       float s = dsa::xor32_sum(0.5f * (s1 + s2));
       const int key = k0 + it * kHTile + 32 * blk + l32;
-      float ksc = 1.f;
-      if (sbase != nullptr) {
-        int32_t raw = lds_read_i32(sc0 + 4 * (st * kHTile + 32 * blk + l32));
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(raw));
-        ksc = __int_as_float(raw);
-      }
+      int32_t raw = lds_read_i32(sc0 + 4 * (st * kHTile + 32 * blk + l32));
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(raw));
+      const float ksc = __int_as_float(raw);
       const float v = key < L ? s * ksc : -__builtin_inff();
       const int off = hh == 0 ? (it * kHTile + 32 * blk + l32) * 4 : 0x40000000;
       __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ost, off, 0, 0);
