@@ -74,6 +74,35 @@ def test_128_heads_short_causal_rows(gpu, S, topk, q_start):
     assert torch.count_nonzero(out[0, r]) == 0 and torch.isinf(lse[0, r]).all()
 
 
+def test_prefill_list_order_cases(gpu):
+    # multi-token lists are gathered in index order (64 buckets of each list's
+    # index range, -1 entries dropped): duplicates, a one-value list, narrow and
+    # very wide ranges, holes and a lone valid entry keep their meaning, and two
+    # launches give bit-identical results (the order is a function of the list)
+    S, Skv, topk = 8, 200000, 512
+    inp = inputs.mla_prefill(B=1, S=S, Skv=Skv, H=128, topk=topk, seed=21, q_start=Skv - S)
+    g = torch.Generator().manual_seed(21)
+    idx = torch.randint(0, Skv, (1, S, 1, topk), generator=g, dtype=torch.int32)
+    idx[0, 1, 0] = torch.randint(0, Skv, (topk // 2,), generator=g, dtype=torch.int32).repeat(2)  # duplicates
+    idx[0, 2, 0] = 777                                                        # one value, 512 times
+    idx[0, 3, 0] = torch.randint(1000, 1040, (topk,), generator=g, dtype=torch.int32)  # span < 64
+    idx[0, 4, 0, : topk // 2] = torch.arange(topk // 2, dtype=torch.int32)    # both ends of the range
+    idx[0, 4, 0, topk // 2:] = torch.arange(Skv - topk // 2, Skv, dtype=torch.int32)
+    idx[0, 5, 0, ::2] = -1                                                    # holes
+    idx[0, 6, 0] = -1
+    idx[0, 6, 0, topk // 2] = 4242                                            # one valid entry
+    idx[0, 7] = idx[0, 7, :, torch.randperm(topk, generator=g)]               # a shuffled list
+    inp["indices"] = idx
+    out, lse = _check(inp, gpu, is_causal=False)
+    out2, lse2 = dsa.sparse_mla_fwd(inp["q"].to(gpu), inp["kv"].to(gpu), idx.to(gpu), inp["sm_scale"],
+                                    is_causal=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2.cpu()) and torch.equal(lse, lse2.cpu())
+    # the one-value row: the softmax over 512 copies of one key is that key's value row
+    torch.testing.assert_close(out[0, 2].float(), inp["kv"][0, 777, 0, :512].float().expand(128, 512),
+                               rtol=1e-2, atol=1e-2)
+
+
 def test_causal_mask_applies(gpu):
     inp = inputs.mla_prefill(B=1, S=16, Skv=512, H=16, topk=64, seed=13)
     g = torch.Generator().manual_seed(0)
