@@ -51,7 +51,7 @@ constexpr int kTileBytes = kKeyTile * kDim;      // 8 KB
 constexpr int kKeyLoaders = kTileBytes / 1024;   // 1 KB loads per tile (waves 0..7 or 8..15)
 constexpr int kSplits = 4;                       // fp8 pieces of u
 constexpr int kE4m3Max = 448;
-constexpr int kMaxChunk = 32768;                 // keys per workgroup at most
+constexpr int kMaxChunk = 131072;                // keys per workgroup at most
 constexpr int kMaxChunkPaged = 16384;            // paged keys: the chunk's pool rows are held in LDS
 
 struct IndexerParams {
@@ -912,9 +912,10 @@ int indexer_fp8_launch(const uint8_t* q, const uint8_t* k, const float* key_scal
   // group-maxima flush) is worth amortising over a longer chunk: with 32 query
   // rows x 128K keys, 256 workgroups of 1024 keys take 39 us where 1024 of 256
   // keys took 70.
-  // Long chunks also cut the re-reads of the query block (read once per chunk):
-  // at 128K keys, 16384-key chunks take 3.44 ms against 3.61 with 4096, 32768-key
-  // chunks another ~1 % less.
+  // Long chunks also cut the re-reads of the query block (read once per chunk)
+  // and the workgroups' fixed costs: at 128K keys, 16384-key chunks take 3.44 ms
+  // against 3.61 with 4096; 32768, 65536 and 131072-key chunks 3304, 3271 and
+  // 3244 us (one workgroup per token block and CU).
   int chunk = block_table != nullptr ? kMaxChunkPaged : kMaxChunk;
   while (chunk > kKeyTile && (int64_t)B * p.ntb * ((S2 + chunk - 1) / chunk) < 256) chunk >>= 1;
   p.chunk = chunk;
