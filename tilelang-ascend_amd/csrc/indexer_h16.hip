@@ -36,7 +36,7 @@ constexpr int kHTile = 64;                      // keys per LDS tile
 constexpr int kHStages = 3;
 constexpr int kHTileBytes = kHTile * kHDim * 2;  // 16 KB
 constexpr int kHLoadsPerTile = kHTileBytes / 1024 / kHWaves;  // 1 KB loads per wave and tile: 2
-constexpr int kHMaxChunk = 32768;
+constexpr int kHMaxChunk = 131072;
 constexpr int kHMaxChunkPaged = 16384;  // the chunk's pool rows are held in LDS
 
 struct H16Params {
