@@ -354,8 +354,10 @@ def summarize_profile(root: str) -> str:
 def summarize_trace(path: str, layer_steps: int) -> str:
     """Per (phase, kernel, workgroups) durations from the rocprofv3 kernel trace
     (``*kernel_trace.csv``) of a bench.py run: the first ``layer_steps`` x 7 DSA
-    dispatches are the layer steps (warmup and timed), the rest the target shapes;
-    torch, runtime-copy and BLAS helper kernels are left out."""
+    dispatches are the layer steps (warmup and timed; in each step the first three
+    are the prefill chunk, phase "layer", and the last four the decode step, phase
+    "decode"), the rest the target shapes; torch, runtime-copy and BLAS helper
+    kernels are left out."""
     import csv
     import glob
 
@@ -370,7 +372,7 @@ def summarize_trace(path: str, layer_steps: int) -> str:
         name = r["Kernel_Name"].replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
         grid = int(r.get("Grid_Size_X") or r.get("Grid_Size") or 0)
         wg = int(r.get("Workgroup_Size_X") or r.get("Workgroup_Size") or 1)
-        phase = "layer" if i < 7 * layer_steps else "target"
+        phase = ("layer" if i % 7 < 3 else "decode") if i < 7 * layer_steps else "target"
         d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
         agg.setdefault((phase, name, grid // max(wg, 1), wg), []).append((d, r))
     lines = [f"{'phase':6s} {'kernel':36s} {'workgroups':>10s} {'wg_size':>7s} {'calls':>5s} {'avg_us':>9s} "
