@@ -299,6 +299,29 @@ def test_long_rows_group_max_selection(gpu, S2, mode):
         _logit_close(lg[t, :n], ref)
 
 
+def test_full_length_key_chunks(gpu):
+    # 2048 query rows x 140000 keys: 128 token blocks keep the longest key chunk
+    # (131072 keys; two chunks per block, the second of 8928 keys), so a workgroup
+    # runs 2048 tiles and every row crosses a chunk boundary.  Logits of the first,
+    # a middle and the last row against the oracle; every row's indices (the
+    # group-maxima top-k) against the stable sort of the kernel's own logits.
+    S1, S2, K = 2048, 140000, 2048
+    q_start = S2 - S1
+    inp = inputs.indexer_fp8(B=1, S1=S1, S2=S2, seed=140, device=gpu)
+    print(f"indexer full-length chunks S1={S1} S2={S2}", flush=True)
+    idx, _, logits = dsa.lightning_indexer(inp["q"], inp["k"], inp["w"], key_scale=inp["key_scale"],
+                                           sparse_count=K, sparse_mode=3, return_logits=True)
+    torch.cuda.synchronize()
+    kdq = inp["k"][0, :, 0].float().cpu() * inp["key_scale"][0].cpu().unsqueeze(1)
+    for t in (0, 1100, S1 - 1):
+        n = q_start + t + 1
+        qk = torch.relu(inp["q"][0, t].float().cpu() @ kdq[:n].T)
+        ref = (inp["w"][0, t].cpu().unsqueeze(1) * qk).sum(0)
+        _logit_close(logits[0, t, :n].cpu().unsqueeze(0), ref.unsqueeze(0))
+    check_topk_rows(idx.view(S1, K), logits.view(S1, S2), q_start + 1 + torch.arange(S1, device=gpu), K,
+                    chunk=64, what="full-length chunks top-k")
+
+
 def test_group_maxima_are_exact(gpu):
     # the indexer's 16-key group maxima equal the maxima of the logits it wrote
     # (every group that holds a visible key; -inf past a row's causal length)

@@ -188,3 +188,29 @@ def test_fp8_fewer_heads(gpu):
         n = int(torch.isfinite(ref).sum())
         scale = float(ref[:n].abs().max())
         assert float((lg[t, :n] - ref[:n]).abs().max()) <= 1e-2 * scale, f"row {t}"
+
+
+def test_full_length_key_chunks(gpu):
+    # 2048 causal bf16 rows x 140000 keys: 256 workgroups of 8 tokens keep the
+    # longest key chunk (131072 keys; two chunks per block, the second of 8928
+    # keys), so every row crosses a chunk boundary.  Logits of three rows against
+    # the oracle's formula at 1e-4 of the row's largest magnitude; every row's
+    # indices against the stable sort of the kernel's own logits.
+    from fullsize import check_topk_rows
+    g = torch.Generator(device=gpu).manual_seed(11)
+    S1, S2, N1, D, K = 2048, 140000, 64, 128, 2048
+    q_start = S2 - S1
+    print(f"indexer bf16 full-length chunks S1={S1} S2={S2}", flush=True)
+    q = torch.randn((1, S1, N1, D), generator=g, device=gpu).to(torch.bfloat16)
+    k = torch.randn((1, S2, 1, D), generator=g, device=gpu).to(torch.bfloat16)
+    w = torch.randn((1, S1, N1), generator=g, device=gpu) / 8
+    idx, _, logits = dsa.lightning_indexer(q, k, w, sparse_count=K, sparse_mode=3, return_logits=True)
+    torch.cuda.synchronize()
+    kc = k[0, :, 0].float().cpu()
+    for t in (0, 1100, S1 - 1):
+        n = q_start + t + 1
+        ref = (w[0, t].cpu().unsqueeze(1) * torch.relu(q[0, t].float().cpu() @ kc[:n].T)).sum(0)
+        got = logits[0, t, :n].cpu()
+        assert float((got - ref).abs().max()) <= 1e-4 * float(ref.abs().max()), f"row {t}"
+    check_topk_rows(idx.view(S1, K), logits.view(S1, S2), q_start + 1 + torch.arange(S1, device=gpu), K,
+                    chunk=64, what="bf16 full-length chunks top-k")
