@@ -700,8 +700,11 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sparse_mla_kernel(MlaPa
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kW4Stages = 4;  // ring stages of the 4-wave form
-constexpr int kW4KPre = 4;    // score A fragments in flight
-constexpr int kW4VPre = 4;    // P.V A fragments (two reads each) in flight
+// LDS fragment reads in flight per wave.  With one wave per SIMD nothing else
+// covers a read's latency; 6 / 5 measured 0.3-1 % faster than 4 / 4 at 128K and
+// at config 4 (the kernel then holds 252 VGPRs), 7 was slower and 7 / 6 spills.
+constexpr int kW4KPre = 6;    // score A fragments in flight
+constexpr int kW4VPre = 5;    // P.V A fragments (two reads each) in flight
 
 // The MFMAs of this form are issued as inline asm so that the register file stays
 // partitioned as designed.  The 256 O^T accumulators are not C++ values at all:
