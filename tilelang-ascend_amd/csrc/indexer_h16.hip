@@ -22,7 +22,8 @@
 // keys of one B-operand read hit distinct banks.  Per 32-key block a wave issues
 // 16 v_mfma_f32_32x32x16 (2 head tiles x 8 k-steps); a lane then holds 16 heads'
 // q.k of one key per tile, applies ReLU and the weights, and one permlane swap
-// adds the other half of the heads.
+// adds the other half of the heads.  That epilogue runs one block behind, its
+// FMAs interleaved with the next block's MFMAs (two accumulator sets).
 #include "dsa_common.h"
 
 namespace {
@@ -258,6 +259,26 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
 #pragma unroll
   for (int i = 0; i < kHStages - 1; ++i) issue(i);
 
+  // Block b's epilogue (its 64 FMAs) runs beside block b + 1's MFMAs: the
+  // accumulators alternate between two sets by block parity, and the first
+  // block's "previous" epilogue stores to an offset the buffer range drops.
+  dsa::f32x16 acc[2][2] = {};
+  float pksc[2] = {0.f, 0.f};
+  int pkey[2] = {0, 0}, poff[2] = {0x40000000, 0x40000000};
+  // sum_h w_h ReLU(d_h) = (sum_h w_h d_h + sum_h w_h |d_h|) / 2 (|.| is a free
+  // source modifier; max would also need a canonicalising instruction), element e
+  // of both head tiles
+  auto fma_pair = [&](const dsa::f32x16& a0, const dsa::f32x16& a1, int e, float& s1, float& s2) {
+    s1 = fmaf(wv[0][e], a0[e], s1);
+    s2 = fmaf(wv[0][e], fabsf(a0[e]), s2);
+    s1 = fmaf(wv[1][e], a1[e], s1);
+    s2 = fmaf(wv[1][e], fabsf(a1[e]), s2);
+  };
+  auto finish = [&](float s1, float s2, float ksc, int key, int off) {
+    float s = dsa::xor32_sum(0.5f * (s1 + s2));
+    const float v = key < L ? s * ksc : -__builtin_inff();
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ost, off, 0, 0);
+  };
   for (int it = 0; it < ntiles; ++it) {
     // tile it's loads are done once the younger ones may remain: the next tile's
     // loads and the two stores of each of the (at most two) tiles finished since
@@ -269,42 +290,46 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
     const uint32_t tb0 = tile0 + st * kHTileBytes;
     dsa::static_for<0, 2>([&](auto BLK) {
       constexpr int blk = decltype(BLK)::value;
-      // the B fragments as asm reads with counted waits: a compiler-issued LDS
-      // read would first wait for every LDS-DMA load in flight (the prefetched
-      // tiles included)
+      constexpr int pb = 1 - blk;  // the previous block's set
+      // the key scale and the B fragments as asm reads with counted waits (a
+      // compiler-issued LDS read would first wait for every LDS-DMA load in
+      // flight, the prefetched tiles included); the scale, read first, is
+      // complete once the first fragment is
       const uint32_t rowa = tb0 + (32 * blk + l32) * (kHDim * 2);
+      int32_t raw = lds_read_i32(sc0 + 4 * (st * kHTile + 32 * blk + l32));
       dsa::i32x4 kb[8];
       dsa::static_for<0, 8>([&](auto KS) {
         constexpr int ks = decltype(KS)::value;
         kb[ks] = dsa::lds_read_b128<0>(rowa + 16 * ((2 * ks + hh) ^ (l32 & 15)));
       });
-      dsa::f32x16 acc0 = {}, acc1 = {};
+      dsa::f32x16 a0 = {}, a1 = {};
+      float s1 = 0.f, s2 = 0.f;
       dsa::static_for<0, 8>([&](auto KS) {
         constexpr int ks = decltype(KS)::value;
-        dsa::lds_wait1<7 - ks>(kb[ks]);
-        acc0 = mfma32<F16>(qa[0][ks], kb[ks], acc0);
-        acc1 = mfma32<F16>(qa[1][ks], kb[ks], acc1);
+        if constexpr (ks == 0)
+          asm volatile("s_waitcnt lgkmcnt(7)" : "+v"(kb[0]), "+v"(raw));
+        else
+          dsa::lds_wait1<7 - ks>(kb[ks]);
+        a0 = mfma32<F16>(qa[0][ks], kb[ks], a0);
+        a1 = mfma32<F16>(qa[1][ks], kb[ks], a1);
+        fma_pair(acc[pb][0], acc[pb][1], 2 * ks, s1, s2);
+        fma_pair(acc[pb][0], acc[pb][1], 2 * ks + 1, s1, s2);
         __builtin_amdgcn_sched_barrier(0);
       });
-      // sum_h w_h ReLU(d_h) = (sum_h w_h d_h + sum_h w_h |d_h|) / 2 (|.| is a free
-      // source modifier; max would also need a canonicalising instruction)
-      float s1 = 0.f, s2 = 0.f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        s1 = fmaf(wv[0][e], acc0[e], s1);
-        s2 = fmaf(wv[0][e], fabsf(acc0[e]), s2);
-        s1 = fmaf(wv[1][e], acc1[e], s1);
-        s2 = fmaf(wv[1][e], fabsf(acc1[e]), s2);
-      }
-      float s = dsa::xor32_sum(0.5f * (s1 + s2));
-      const int key = k0 + it * kHTile + 32 * blk + l32;
-      int32_t raw = lds_read_i32(sc0 + 4 * (st * kHTile + 32 * blk + l32));
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(raw));
-      const float ksc = __int_as_float(raw);
-      const float v = key < L ? s * ksc : -__builtin_inff();
-      const int off = hh == 0 ? (it * kHTile + 32 * blk + l32) * 4 : 0x40000000;
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ost, off, 0, 0);
+      finish(s1, s2, pksc[pb], pkey[pb], poff[pb]);
+      acc[blk][0] = a0;
+      acc[blk][1] = a1;
+      pksc[blk] = __int_as_float(raw);
+      pkey[blk] = k0 + it * kHTile + 32 * blk + l32;
+      poff[blk] = hh == 0 ? (it * kHTile + 32 * blk + l32) * 4 : 0x40000000;
     });
+  }
+  {
+    // the last block's epilogue
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) fma_pair(acc[1][0], acc[1][1], e, s1, s2);
+    finish(s1, s2, pksc[1], pkey[1], poff[1]);
   }
   // no LDS DMA may still be in flight when the workgroup's LDS is released
   dsa::wait_vmcnt<0>();
