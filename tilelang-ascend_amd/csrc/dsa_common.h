@@ -44,6 +44,30 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
+// Workspace of the full lightning indexer (both the fp8 and the 16-bit entry
+// points): fp32 logits [rows, S2] | int32 row_len [rows] | fp32 maxima of 16-key
+// groups [rows, ceil(S2 / 16)], each part 256-byte aligned.
+struct IndexerWorkspace {
+  size_t rowlen_off, gmax_off, bytes;
+  int64_t ld_g;
+};
+
+inline IndexerWorkspace indexer_workspace(int64_t rows_in, int64_t S2_in) {
+  const size_t rows = (size_t)(rows_in < 0 ? 0 : rows_in);
+  const size_t S2 = (size_t)(S2_in < 0 ? 0 : S2_in);
+  auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
+  IndexerWorkspace w;
+  w.ld_g = (int64_t)((S2 + 15) / 16);
+  w.rowlen_off = up(rows * S2 * sizeof(float));
+  w.gmax_off = w.rowlen_off + up(rows * sizeof(int32_t));
+  w.bytes = w.gmax_off + rows * (size_t)w.ld_g * sizeof(float);
+  return w;
+}
+
+// The top-k reads the group maxima (and only the groups that can hold a top-K
+// element) when a row has at least 2 K groups; below that it streams the row.
+inline bool use_group_max(int64_t S2, int32_t K) { return (S2 + 15) / 16 >= 2 * (int64_t)K; }
+
 // The MI355X has 8 XCDs; consecutive workgroup ids are dealt round-robin to
 // them.  Kernels that want related workgroups to share one XCD's L2 regroup
 // their linear id with this constant.

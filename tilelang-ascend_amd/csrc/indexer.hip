@@ -991,30 +991,9 @@ int topk_launch(const float* x, int64_t rows, int64_t cols, int64_t ld, const in
                 float* out_val, hipStream_t stream);
 }
 
-namespace {
-// Workspace of the full indexer: fp32 logits [rows, S2] | int32 row_len [rows] |
-// fp32 maxima of 16-key groups [rows, ceil(S2 / 16)], each part 256-byte aligned.
-struct IndexerWorkspace {
-  size_t rowlen_off, gmax_off, bytes;
-  int64_t ld_g;
-};
-
-IndexerWorkspace indexer_workspace(int64_t rows_in, int64_t S2_in) {
-  const size_t rows = (size_t)(rows_in < 0 ? 0 : rows_in);
-  const size_t S2 = (size_t)(S2_in < 0 ? 0 : S2_in);
-  auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
-  IndexerWorkspace w;
-  w.ld_g = (int64_t)((S2 + 15) / 16);
-  w.rowlen_off = up(rows * S2 * sizeof(float));
-  w.gmax_off = w.rowlen_off + up(rows * sizeof(int32_t));
-  w.bytes = w.gmax_off + rows * (size_t)w.ld_g * sizeof(float);
-  return w;
-}
-
-// The top-k reads the group maxima (and only the groups that can hold a top-K
-// element) when a row has at least 2 K groups; below that it streams the row.
-bool use_group_max(int64_t S2, int32_t K) { return (S2 + 15) / 16 >= 2 * (int64_t)K; }
-}  // namespace
+using dsa::IndexerWorkspace;
+using dsa::indexer_workspace;
+using dsa::use_group_max;
 
 extern "C" size_t dsa_lightning_indexer_workspace_bytes(int64_t B, int64_t S1, int64_t S2) {
   return indexer_workspace((B < 0 ? 0 : B) * (S1 < 0 ? 0 : S1), S2).bytes;

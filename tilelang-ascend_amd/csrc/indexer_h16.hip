@@ -26,6 +26,8 @@
 // FMAs interleaved with the next block's MFMAs (two accumulator sets).
 #include "dsa_common.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int kHWaves = 8;
@@ -54,7 +56,9 @@ struct H16Params {
   int block_size, max_blocks;
   float* logits;      // [q rows, ld]
   int32_t* row_len;   // [q rows] or null
+  float* gmax;        // [q rows, ld_g] maxima of 16-key groups, or null
   int64_t ld;
+  int64_t ld_g;
   int B, S1, S2, N1, sparse_mode;
   int chunk, ntb, nkc;
   int64_t per_xcd;
@@ -81,7 +85,11 @@ __device__ __forceinline__ void wait_vmcnt_rt(int n) {
     case 4: dsa::wait_vmcnt<4>(); break;
     case 5: dsa::wait_vmcnt<5>(); break;
     case 6: dsa::wait_vmcnt<6>(); break;
-    default: dsa::wait_vmcnt<7>(); break;
+    case 7: dsa::wait_vmcnt<7>(); break;
+    case 8: dsa::wait_vmcnt<8>(); break;
+    case 9: dsa::wait_vmcnt<9>(); break;
+    case 10: dsa::wait_vmcnt<10>(); break;
+    default: dsa::wait_vmcnt<11>(); break;
   }
 }
 
@@ -105,7 +113,7 @@ __device__ __forceinline__ int32_t lds_read_i32(uint32_t addr) {
 __device__ __align__(16) uint16_t g_zero_key16[kHDim];
 __device__ float g_zero_scale16[kHTile];
 
-template <bool F16, bool PAGED>
+template <bool F16, bool PAGED, bool GMAX>
 __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
   __shared__ __align__(1024) uint8_t ktile[kHStages][kHTileBytes];
   __shared__ __align__(256) float kscale[kHStages][kHTile];
@@ -255,16 +263,27 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
   float* orow = p.logits + trow * p.ld + k0;
   const __amdgpu_buffer_rsrc_t ost =
       __builtin_amdgcn_make_buffer_rsrc(orow, (short)0, tok_ok ? (kend - k0) * 4 : 0, 0x00020000);
+  // group maxima: one float per 16 keys (the chunk start is a multiple of 64)
+  const __amdgpu_buffer_rsrc_t gst = __builtin_amdgcn_make_buffer_rsrc(
+      GMAX ? p.gmax + trow * p.ld_g + k0 / 16 : p.logits, (short)0,
+      (GMAX && tok_ok) ? ((kend - k0 + 15) / 16) * 4 : 0, 0x00020000);
+  // stores per tile: a logit (and a group-maxima) store
+  constexpr int kStoresPerTile = GMAX ? 2 : 1;
 
 #pragma unroll
   for (int i = 0; i < kHStages - 1; ++i) issue(i);
 
-  // Block b's epilogue (its 64 FMAs) runs beside block b + 1's MFMAs: the
-  // accumulators alternate between two sets by block parity, and the first
-  // block's "previous" epilogue stores to an offset the buffer range drops.
+  // Block b's 64 FMAs run beside block b + 1's MFMAs (the accumulators alternate
+  // between two sets by block parity), and a tile's epilogue runs once its second
+  // block's FMAs are done, in the next tile: a permlane swap adds the two head
+  // halves of both blocks at once, leaving block 0's logits in lanes 0-31 and
+  // block 1's in lanes 32-63 (lane l holds key l of the tile), so the tile takes
+  // one key-scale read, one 256-byte logit store and one group-maxima pass.  The
+  // first tile's "previous" epilogue stores to offsets the buffer range drops.
   dsa::f32x16 acc[2][2] = {};
-  float pksc[2] = {0.f, 0.f};
-  int pkey[2] = {0, 0}, poff[2] = {0x40000000, 0x40000000};
+  float hA = 0.f;  // this lane's half-head sum of block 0 of the current tile
+  float tksc = 0.f;  // the previous tile's key scale, key and store offsets
+  int tkey = 0, toff = 0x40000000, tgoff = 0x40000000;
   // sum_h w_h ReLU(d_h) = (sum_h w_h d_h + sum_h w_h |d_h|) / 2 (|.| is a free
   // source modifier; max would also need a canonicalising instruction), element e
   // of both head tiles
@@ -274,15 +293,36 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
     s1 = fmaf(wv[1][e], a1[e], s1);
     s2 = fmaf(wv[1][e], fabsf(a1[e]), s2);
   };
-  auto finish = [&](float s1, float s2, float ksc, int key, int off) {
-    float s = dsa::xor32_sum(0.5f * (s1 + s2));
+  // hA / hB: half-head sums of the tile's blocks 0 and 1 (lane l < 32: heads of
+  // the lower half, l >= 32: the upper half, key l % 32)
+  auto finish_tile = [&](float a, float b, float ksc, int key, int off, int goff) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    const float s = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     const float v = key < L ? s * ksc : -__builtin_inff();
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ost, off, 0, 0);
+    if constexpr (GMAX) {
+      // max over each row of 16 lanes (16 consecutive keys): v_max_f32 with DPP
+      // quad swaps, then half-row and row mirrors (each DPP source written two
+      // wait states earlier).  v_max_f32 returns the non-NaN operand, and the
+      // top-k orders NaN last, so a NaN logit never raises a group's maximum.
+      float m = v;
+      asm volatile(
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+          "s_nop 1\n"
+          "v_max_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf"
+          : "+v"(m));
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), gst, goff, 0, 0);
+    }
   };
   for (int it = 0; it < ntiles; ++it) {
     // tile it's loads are done once the younger ones may remain: the next tile's
-    // loads and the two stores of each of the (at most two) tiles finished since
-    wait_vmcnt_rt(nload + (it == 0 ? 0 : (it == 1 ? 2 : 4)));
+    // loads and the stores of each of the (at most two) tiles finished since
+    wait_vmcnt_rt(nload + (it == 0 ? 0 : (it == 1 ? kStoresPerTile : 2 * kStoresPerTile)));
     // a bare barrier: __syncthreads() would also drain the prefetched tiles
     __builtin_amdgcn_s_barrier();
     issue(it + kHStages - 1);
@@ -291,12 +331,14 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
     dsa::static_for<0, 2>([&](auto BLK) {
       constexpr int blk = decltype(BLK)::value;
       constexpr int pb = 1 - blk;  // the previous block's set
-      // the key scale and the B fragments as asm reads with counted waits (a
+      // the B fragments (and in block 1 the tile's 64 key scales, read first and
+      // complete once the first fragment is) as asm reads with counted waits: a
       // compiler-issued LDS read would first wait for every LDS-DMA load in
-      // flight, the prefetched tiles included); the scale, read first, is
-      // complete once the first fragment is
+      // flight, the prefetched tiles included.  The scales are read before the
+      // next tile's loads can overwrite their ring stage.
       const uint32_t rowa = tb0 + (32 * blk + l32) * (kHDim * 2);
-      int32_t raw = lds_read_i32(sc0 + 4 * (st * kHTile + 32 * blk + l32));
+      int32_t raw = 0;
+      if constexpr (blk == 1) raw = lds_read_i32(sc0 + 4 * (st * kHTile + lane));
       dsa::i32x4 kb[8];
       dsa::static_for<0, 8>([&](auto KS) {
         constexpr int ks = decltype(KS)::value;
@@ -306,7 +348,7 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
       float s1 = 0.f, s2 = 0.f;
       dsa::static_for<0, 8>([&](auto KS) {
         constexpr int ks = decltype(KS)::value;
-        if constexpr (ks == 0)
+        if constexpr (ks == 0 && blk == 1)
           asm volatile("s_waitcnt lgkmcnt(7)" : "+v"(kb[0]), "+v"(raw));
         else
           dsa::lds_wait1<7 - ks>(kb[ks]);
@@ -316,20 +358,27 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
         fma_pair(acc[pb][0], acc[pb][1], 2 * ks + 1, s1, s2);
         __builtin_amdgcn_sched_barrier(0);
       });
-      finish(s1, s2, pksc[pb], pkey[pb], poff[pb]);
       acc[blk][0] = a0;
       acc[blk][1] = a1;
-      pksc[blk] = __int_as_float(raw);
-      pkey[blk] = k0 + it * kHTile + 32 * blk + l32;
-      poff[blk] = hh == 0 ? (it * kHTile + 32 * blk + l32) * 4 : 0x40000000;
+      if constexpr (blk == 0) {
+        // the FMAs just done were block 1 of the previous tile: its epilogue
+        finish_tile(hA, 0.5f * (s1 + s2), tksc, tkey, toff, tgoff);
+      } else {
+        hA = 0.5f * (s1 + s2);  // block 0 of this tile
+        tksc = __int_as_float(raw);
+        tkey = k0 + it * kHTile + lane;
+        toff = (it * kHTile + lane) * 4;
+        // lanes 0, 16, 32 and 48 store the tile's four groups
+        tgoff = (lane & 15) == 0 ? (it * (kHTile / 16) + (lane >> 4)) * 4 : 0x40000000;
+      }
     });
   }
   {
-    // the last block's epilogue
+    // the last tile's block 1 and epilogue
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) fma_pair(acc[1][0], acc[1][1], e, s1, s2);
-    finish(s1, s2, pksc[1], pkey[1], poff[1]);
+    finish_tile(hA, 0.5f * (s1 + s2), tksc, tkey, toff, tgoff);
   }
   // no LDS DMA may still be in flight when the workgroup's LDS is released
   dsa::wait_vmcnt<0>();
@@ -361,19 +410,23 @@ int indexer_h16_launch(const H16Params& base, bool f16, hipStream_t stream) {
   if (nblocks <= 0) return kOk;
   if (nblocks > 0x7fffffff) return set_error(kUnsupported, "indexer (16-bit): grid too large");
   const dim3 grid((unsigned)nblocks), blk(kHThreads);
-  const bool paged = p.block_table != nullptr;
-  if (f16 && paged) hipLaunchKernelGGL((indexer_h16_kernel<true, true>), grid, blk, 0, stream, p);
-  else if (f16) hipLaunchKernelGGL((indexer_h16_kernel<true, false>), grid, blk, 0, stream, p);
-  else if (paged) hipLaunchKernelGGL((indexer_h16_kernel<false, true>), grid, blk, 0, stream, p);
-  else hipLaunchKernelGGL((indexer_h16_kernel<false, false>), grid, blk, 0, stream, p);
+  const bool paged = p.block_table != nullptr, gm = p.gmax != nullptr;
+  auto go = [&](auto F16C, auto PAGEDC, auto GMAXC) {
+    hipLaunchKernelGGL((indexer_h16_kernel<decltype(F16C)::value, decltype(PAGEDC)::value, decltype(GMAXC)::value>),
+                       grid, blk, 0, stream, p);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  if (f16) {
+    if (paged) gm ? go(T{}, T{}, T{}) : go(T{}, T{}, F{});
+    else gm ? go(T{}, F{}, T{}) : go(T{}, F{}, F{});
+  } else {
+    if (paged) gm ? go(F{}, T{}, T{}) : go(F{}, T{}, F{});
+    else gm ? go(F{}, F{}, T{}) : go(F{}, F{}, F{});
+  }
   return check_launch("dsa_lightning_indexer_h16_varlen");
 }
 
-// Workspace layout shared with the fp8 entry points: fp32 logits [rows, S2] |
-// int32 row_len [rows] | (group maxima, unused here), parts 256-byte aligned.
-size_t rowlen_offset(int64_t rows, int64_t S2) {
-  return ((size_t)rows * (size_t)S2 * sizeof(float) + 255) & ~size_t(255);
-}
 
 }  // namespace
 
@@ -414,8 +467,12 @@ extern "C" int dsa_lightning_indexer_h16_varlen(const void* q, const void* k, co
   if (workspace == nullptr || workspace_bytes < need)
     return set_error(kWorkspaceTooSmall, "%s: workspace of %zu bytes needed, %zu given", what, need, workspace_bytes);
   if (indices == nullptr) return set_error(kInvalidArgument, "%s: null indices", what);
+  // the fp8 entry points' workspace layout (logits | row lengths | group maxima)
+  const IndexerWorkspace wl = indexer_workspace(q_rows, S2);
   float* logits = static_cast<float*>(workspace);
-  int32_t* row_len = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + rowlen_offset(q_rows, S2));
+  int32_t* row_len = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + wl.rowlen_off);
+  float* gmax = use_group_max(S2, sparse_count) ? reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.gmax_off)
+                                                : nullptr;
   hipStream_t st = (hipStream_t)stream;
   if (S2 == 0 || B == 0 || S1 == 0)  // no keys (or no rows to score): every row is all -1
     return topk_launch(logits, q_rows, 0, 0, nullptr, nullptr, 0, sparse_count, 1, indices, values, st);
@@ -439,7 +496,9 @@ extern "C" int dsa_lightning_indexer_h16_varlen(const void* q, const void* k, co
   p.pool_rows = pool_rows;
   p.logits = logits;
   p.row_len = row_len;
+  p.gmax = gmax;
   p.ld = S2;
+  p.ld_g = wl.ld_g;
   p.B = (int)B;
   p.S1 = (int)S1;
   p.S2 = (int)S2;
@@ -447,5 +506,5 @@ extern "C" int dsa_lightning_indexer_h16_varlen(const void* q, const void* k, co
   p.sparse_mode = sparse_mode;
   const int rc = indexer_h16_launch(p, is_f16 != 0, st);
   if (rc != kOk) return rc;
-  return topk_launch(logits, q_rows, S2, S2, row_len, nullptr, 0, sparse_count, 1, indices, values, st);
+  return topk_launch(logits, q_rows, S2, S2, row_len, gmax, wl.ld_g, sparse_count, 1, indices, values, st);
 }
