@@ -591,8 +591,9 @@ def indexer_h16_config(L, steps: int) -> dict:
     """The indexer at the reference wrapper's own precision (bf16 q and k,
     examples/deepseek_v4/lightning_indexer.py:1250-1253) at config-5 size: 4096 tail
     queries x 131072 keys, 64 heads x 128, causal, top-2048 (the full entry: the
-    16-bit MFMA logits kernel, then the streamed top-k; no group maxima).  The top-k
-    alone on the same logits is timed too; the indexer's share is the difference.
+    16-bit MFMA logits kernel with its 16-key group maxima, then the group-maxima
+    top-k).  That top-k alone on the same logits and maxima is timed too; the
+    indexer's share is the difference.
     FLOP = 2 * 64 * 128 per visible pair, against the 2.5 PFLOP/s 16-bit MFMA peak."""
     import torch
 
@@ -607,7 +608,12 @@ def indexer_h16_config(L, steps: int) -> dict:
     wsb = L.dsa_lightning_indexer_varlen_workspace_bytes(S1, S2)
     ws = torch.empty((wsb,), dtype=torch.uint8, device=dev)
     logits = ws[: S1 * S2 * 4].view(torch.float32)
-    row_len = ws[(S1 * S2 * 4 + 255) // 256 * 256:][: S1 * 4].view(torch.int32)
+    # the entry point's workspace: logits | row lengths | group maxima, 256-byte aligned
+    rl_off = (S1 * S2 * 4 + 255) // 256 * 256
+    gm_off = rl_off + (S1 * 4 + 255) // 256 * 256
+    ld_g = (S2 + 15) // 16
+    row_len = ws[rl_off:][: S1 * 4].view(torch.int32)
+    gmax = ws[gm_off:][: S1 * ld_g * 4].view(torch.float32)
     idx2 = torch.empty((S1, TOPK), dtype=torch.int32, device=dev)
 
     def full():
@@ -618,7 +624,8 @@ def indexer_h16_config(L, steps: int) -> dict:
             raise RuntimeError(f"indexer_h16: {L.dsa_last_error().decode()}")
 
     def tk():
-        rc = L.dsa_topk_f32(logits.data_ptr(), S1, S2, S2, row_len.data_ptr(), TOPK, 1, idx2.data_ptr(), None, st)
+        rc = L.dsa_topk_f32_group_max(logits.data_ptr(), S1, S2, S2, row_len.data_ptr(), gmax.data_ptr(), ld_g, TOPK,
+                                      1, idx2.data_ptr(), None, st)
         if rc != 0:
             raise RuntimeError(f"topk of the h16 logits: {L.dsa_last_error().decode()}")
 
@@ -626,7 +633,9 @@ def indexer_h16_config(L, steps: int) -> dict:
     ut = _time_launches(tk, max(2, steps // 2))
     fl = indexer_flops_causal(S1, S2)
     ui = uf - ut
-    del q, k, w, idx, ws, logits, row_len, idx2
+    if not torch.equal(idx.view(S1, TOPK), idx2):
+        raise RuntimeError("indexer_h16: the timed top-k differs from the entry point's")
+    del q, k, w, idx, ws, logits, row_len, gmax, idx2
     torch.cuda.empty_cache()
     return {"dtype": "bf16", "indexer_topk_us": round(uf, 1), "topk_us": round(ut, 1),
             "indexer_us_derived": round(ui, 1), "indexer_tflops": round(fl / ui / 1e6, 1),
