@@ -214,3 +214,45 @@ def test_full_length_key_chunks(gpu):
         assert float((got - ref).abs().max()) <= 1e-4 * float(ref.abs().max()), f"row {t}"
     check_topk_rows(idx.view(S1, K), logits.view(S1, S2), q_start + 1 + torch.arange(S1, device=gpu), K,
                     chunk=64, what="bf16 full-length chunks top-k")
+
+
+def test_paged_long_rows_group_maxima(gpu):
+    # bf16 keys in shuffled 128-key pages, two sequences of 70000 / 66000 keys,
+    # causal rows: at least 2 K groups of 16 keys per row, so the logits kernel
+    # writes the group maxima and the top-k reads only the groups that can hold a
+    # top-K key.  Paged and contiguous keys give bit-identical logits and indices;
+    # every row's indices equal the stable sort of the kernel's own logits; two
+    # rows' logits against the formula.
+    from fullsize import check_topk_rows
+    rng = np.random.RandomState(9)
+    B, S1, N1, D, K, bs = 2, 24, 64, 128, 2048, 128
+    act_k = [70000, 66000]
+    nblk = sum((a + bs - 1) // bs for a in act_k)
+    print(f"indexer bf16 paged long rows act_k={act_k}", flush=True)
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn((B, S1, N1, D), generator=g).to(torch.bfloat16)
+    w = torch.randn((B, S1, N1), generator=g) / 8
+    k = torch.randn((B, max(act_k), 1, D), generator=g).to(torch.bfloat16)
+    k_pa, bt = _build_pa(k, act_k, bs, nblk, seed=9)
+    asq = torch.full((B,), S1, dtype=torch.int32)
+    ask = torch.tensor(act_k, dtype=torch.int32)
+    d = lambda t: t.to(gpu)  # noqa: E731
+    idx_p, _, lg_p = dsa.lightning_indexer(d(q), d(k_pa), d(w), actual_seq_lengths_query=d(asq),
+                                           actual_seq_lengths_key=d(ask), block_table=d(bt), layout_key="PA_BSND",
+                                           sparse_count=K, sparse_mode=3, return_logits=True)
+    idx_c, _, lg_c = dsa.lightning_indexer(d(q), d(k), d(w), actual_seq_lengths_query=d(asq),
+                                           actual_seq_lengths_key=d(ask), sparse_count=K, sparse_mode=3,
+                                           return_logits=True)
+    torch.cuda.synchronize()
+    L = torch.tensor([act_k[b] - S1 + s + 1 for b in range(B) for s in range(S1)], dtype=torch.int32, device=gpu)
+    lp, lc = lg_p.reshape(B * S1, -1), lg_c.reshape(B * S1, -1)
+    n = min(lp.shape[1], lc.shape[1])
+    keep = torch.arange(n, device=gpu).unsqueeze(0) < L.view(-1, 1)
+    assert torch.equal(torch.where(keep, lp[:, :n], 0.), torch.where(keep, lc[:, :n], 0.)), "paged logits differ"
+    assert torch.equal(idx_p, idx_c), "paged indices differ"
+    check_topk_rows(idx_p.reshape(B * S1, K), lc[:, :n].contiguous(), L, K, chunk=48, what="bf16 paged top-k")
+    for b, s in ((0, 0), (1, S1 - 1)):
+        nl = act_k[b] - S1 + s + 1
+        ref = (w[b, s].unsqueeze(1) * torch.relu(q[b, s].float() @ k[b, :nl, 0].float().T)).sum(0)
+        got = lc[b * S1 + s, :nl].cpu()
+        assert float((got - ref).abs().max()) <= 1e-4 * float(ref.abs().max()), f"row ({b}, {s})"
