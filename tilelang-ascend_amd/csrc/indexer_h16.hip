@@ -21,9 +21,11 @@
 // global_load_lds, chunk c of key s stored at slot c ^ (s % 16) so that the 32
 // keys of one B-operand read hit distinct banks.  Per 32-key block a wave issues
 // 16 v_mfma_f32_32x32x16 (2 head tiles x 8 k-steps); a lane then holds 16 heads'
-// q.k of one key per tile, applies ReLU and the weights, and one permlane swap
-// adds the other half of the heads.  That epilogue runs one block behind, its
-// FMAs interleaved with the next block's MFMAs (two accumulator sets).
+// q.k of one key per tile and applies ReLU and the weights, one block behind, its
+// FMAs interleaved with the next block's MFMAs (two accumulator sets).  Once per
+// 64-key tile one permlane swap adds the other half of the heads for both blocks,
+// and the tile's logits (and, for long rows, the maxima of its four 16-key groups,
+// which the top-k uses as on the fp8 path) are stored.
 #include "dsa_common.h"
 
 #include <type_traits>
