@@ -20,9 +20,10 @@
 // tiles of 64 x 128 16-bit values stream through a 3-stage LDS ring with
 // global_load_lds, chunk c of key s stored at slot c ^ (s % 16) so that the 32
 // keys of one B-operand read hit distinct banks.  Per 32-key block a wave issues
-// 16 v_mfma_f32_32x32x16 (2 head tiles x 8 k-steps); a lane then holds 16 heads'
-// q.k of one key per tile and applies ReLU and the weights, one block behind, its
-// FMAs interleaved with the next block's MFMAs (two accumulator sets).  Once per
+// 16 v_mfma_f32_32x32x16 (2 head tiles x 8 k-steps; one tile when N1 <= 32); a
+// lane then holds 16 heads' q.k of one key per tile and applies ReLU and the
+// weights, one block behind, its FMAs interleaved with the next block's MFMAs
+// (two accumulator sets).  Once per
 // 64-key tile one permlane swap adds the other half of the heads for both blocks,
 // and the tile's logits (and, for long rows, the maxima of its four 16-key groups,
 // which the top-k uses as on the fp8 path) are stored.
@@ -115,8 +116,11 @@ __device__ __forceinline__ int32_t lds_read_i32(uint32_t addr) {
 __device__ __align__(16) uint16_t g_zero_key16[kHDim];
 __device__ float g_zero_scale16[kHTile];
 
-template <bool F16, bool PAGED, bool GMAX>
+// HT: 32-head tiles computed (1 when N1 <= 32: the second tile's heads are all
+// zero and would only add zeros).
+template <bool F16, bool PAGED, bool GMAX, int HT>
 __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
+  static_assert(HT == 1 || HT == 2, "one or two head tiles");
   __shared__ __align__(1024) uint8_t ktile[kHStages][kHTileBytes];
   __shared__ __align__(256) float kscale[kHStages][kHTile];
   __shared__ int32_t krows[PAGED ? kHMaxChunkPaged : 1];
@@ -172,10 +176,10 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
   // ---- per-token operands: A of head tile t, k-step ks = head 32 t + l32, dims
   // 16 ks + 8 hh .. + 8; the weight of result element r of tile t (head
   // 32 t + 8 (r / 4) + 4 hh + r % 4); heads >= N1 are zero
-  dsa::i32x4 qa[2][8];
-  float wv[2][16];
+  dsa::i32x4 qa[HT][8];
+  float wv[HT][16];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < HT; ++t) {
     const int head = 32 * t + l32;
     const bool ok = tok_ok && head < p.N1;
     const uint16_t* qp = p.q + (trow * p.N1 + (ok ? head : 0)) * kHDim + 8 * hh;
@@ -282,7 +286,7 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
   // block 1's in lanes 32-63 (lane l holds key l of the tile), so the tile takes
   // one key-scale read, one 256-byte logit store and one group-maxima pass.  The
   // first tile's "previous" epilogue stores to offsets the buffer range drops.
-  dsa::f32x16 acc[2][2] = {};
+  dsa::f32x16 acc[2][2] = {};  // [block parity][head tile]; tile 1 unused when HT == 1
   float hA = 0.f;  // this lane's half-head sum of block 0 of the current tile
   float tksc = 0.f;  // the previous tile's key scale, key and store offsets
   int tkey = 0, toff = 0x40000000, tgoff = 0x40000000;
@@ -292,8 +296,10 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
   auto fma_pair = [&](const dsa::f32x16& a0, const dsa::f32x16& a1, int e, float& s1, float& s2) {
     s1 = fmaf(wv[0][e], a0[e], s1);
     s2 = fmaf(wv[0][e], fabsf(a0[e]), s2);
-    s1 = fmaf(wv[1][e], a1[e], s1);
-    s2 = fmaf(wv[1][e], fabsf(a1[e]), s2);
+    if constexpr (HT == 2) {
+      s1 = fmaf(wv[HT - 1][e], a1[e], s1);
+      s2 = fmaf(wv[HT - 1][e], fabsf(a1[e]), s2);
+    }
   };
   // hA / hB: half-head sums of the tile's blocks 0 and 1 (lane l < 32: heads of
   // the lower half, l >= 32: the upper half, key l % 32)
@@ -355,7 +361,7 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
         else
           dsa::lds_wait1<7 - ks>(kb[ks]);
         a0 = mfma32<F16>(qa[0][ks], kb[ks], a0);
-        a1 = mfma32<F16>(qa[1][ks], kb[ks], a1);
+        if constexpr (HT == 2) a1 = mfma32<F16>(qa[HT - 1][ks], kb[ks], a1);
         fma_pair(acc[pb][0], acc[pb][1], 2 * ks, s1, s2);
         fma_pair(acc[pb][0], acc[pb][1], 2 * ks + 1, s1, s2);
         __builtin_amdgcn_sched_barrier(0);
@@ -413,9 +419,11 @@ int indexer_h16_launch(const H16Params& base, bool f16, hipStream_t stream) {
   if (nblocks > 0x7fffffff) return set_error(kUnsupported, "indexer (16-bit): grid too large");
   const dim3 grid((unsigned)nblocks), blk(kHThreads);
   const bool paged = p.block_table != nullptr, gm = p.gmax != nullptr;
+  const bool one_tile = p.N1 <= 32;
   auto go = [&](auto F16C, auto PAGEDC, auto GMAXC) {
-    hipLaunchKernelGGL((indexer_h16_kernel<decltype(F16C)::value, decltype(PAGEDC)::value, decltype(GMAXC)::value>),
-                       grid, blk, 0, stream, p);
+    constexpr bool kF16 = decltype(F16C)::value, kPaged = decltype(PAGEDC)::value, kGmax = decltype(GMAXC)::value;
+    if (one_tile) hipLaunchKernelGGL((indexer_h16_kernel<kF16, kPaged, kGmax, 1>), grid, blk, 0, stream, p);
+    else hipLaunchKernelGGL((indexer_h16_kernel<kF16, kPaged, kGmax, 2>), grid, blk, 0, stream, p);
   };
   using T = std::true_type;
   using F = std::false_type;
