@@ -256,3 +256,28 @@ def test_paged_long_rows_group_maxima(gpu):
         ref = (w[b, s].unsqueeze(1) * torch.relu(q[b, s].float() @ k[b, :nl, 0].float().T)).sum(0)
         got = lc[b * S1 + s, :nl].cpu()
         assert float((got - ref).abs().max()) <= 1e-4 * float(ref.abs().max()), f"row ({b}, {s})"
+
+
+@pytest.mark.parametrize("n1", [8, 24])
+def test_few_heads_long_rows(gpu, n1):
+    # N1 <= 32 (the reference examples' head counts) on rows long enough for the
+    # group-maxima top-k: the one-tile kernel with group maxima.  Every row's
+    # indices against the stable sort of the kernel's logits; two rows' logits
+    # against the formula.
+    from fullsize import check_topk_rows
+    g = torch.Generator(device=gpu).manual_seed(n1)
+    S1, S2, K = 24, 70000, 2048
+    print(f"indexer bf16 N1={n1} long rows S2={S2}", flush=True)
+    q = torch.randn((1, S1, n1, 128), generator=g, device=gpu).to(torch.bfloat16)
+    k = torch.randn((1, S2, 1, 128), generator=g, device=gpu).to(torch.bfloat16)
+    w = torch.randn((1, S1, n1), generator=g, device=gpu) / 8
+    idx, _, logits = dsa.lightning_indexer(q, k, w, sparse_count=K, sparse_mode=3, return_logits=True)
+    torch.cuda.synchronize()
+    L = S2 - S1 + 1 + torch.arange(S1, device=gpu)
+    check_topk_rows(idx.view(S1, K), logits.view(S1, S2), L, K, chunk=24, what=f"N1={n1} top-k")
+    kc = k[0, :, 0].float().cpu()
+    for t in (0, S1 - 1):
+        n = S2 - S1 + t + 1
+        ref = (w[0, t].cpu().unsqueeze(1) * torch.relu(q[0, t].float().cpu() @ kc[:n].T)).sum(0)
+        got = logits[0, t, :n].cpu()
+        assert float((got - ref).abs().max()) <= 1e-4 * float(ref.abs().max()), f"row {t}"
