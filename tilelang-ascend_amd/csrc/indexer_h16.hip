@@ -279,7 +279,7 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
 #pragma unroll
   for (int i = 0; i < kHStages - 1; ++i) issue(i);
 
-  // Block b's 64 FMAs run beside block b + 1's MFMAs (the accumulators alternate
+  // Block b's FMAs run beside block b + 1's MFMAs (the accumulators alternate
   // between two sets by block parity), and a tile's epilogue runs once its second
   // block's FMAs are done, in the next tile: a permlane swap adds the two head
   // halves of both blocks at once, leaving block 0's logits in lanes 0-31 and
@@ -292,7 +292,7 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
   int tkey = 0, toff = 0x40000000, tgoff = 0x40000000;
   // sum_h w_h ReLU(d_h) = (sum_h w_h d_h + sum_h w_h |d_h|) / 2 (|.| is a free
   // source modifier; max would also need a canonicalising instruction), element e
-  // of both head tiles
+  // of the head tiles
   auto fma_pair = [&](const dsa::f32x16& a0, const dsa::f32x16& a1, int e, float& s1, float& s2) {
     s1 = fmaf(wv[0][e], a0[e], s1);
     s2 = fmaf(wv[0][e], fabsf(a0[e]), s2);
@@ -301,7 +301,7 @@ __global__ __launch_bounds__(kHThreads) void indexer_h16_kernel(H16Params p) {
       s2 = fmaf(wv[HT - 1][e], fabsf(a1[e]), s2);
     }
   };
-  // hA / hB: half-head sums of the tile's blocks 0 and 1 (lane l < 32: heads of
+  // a / b: the half-head sums of the tile's blocks 0 and 1 (lane l < 32: heads of
   // the lower half, l >= 32: the upper half, key l % 32)
   auto finish_tile = [&](float a, float b, float ksc, int key, int off, int goff) {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
