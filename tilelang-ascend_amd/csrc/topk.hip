@@ -568,11 +568,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ITEMS 
             sv[u] = i < ns ? ordered_key(gpre[u]) : 0u;
           } else {
             const int blk = i >> 6;
-            // blocks shifted by 0-3 x 64 elements: evenly spaced ~4 KB apart (and
-            // rows 128 KB apart) they fell on few memory channels and the sample
-            // took ~7 % more of a 32K row's time.  Blocks span >= 256 elements
-            // (nb <= L / 256), so a shifted block stays inside the row.
-            const int start = (int)(((int64_t)blk * L / nb) & ~63) + 64 * (blk & 3);
+            const int start = (int)(((int64_t)blk * L / nb) & ~63);
             sv[u] = i < ns ? ordered_key(xr[start + (i & 63)]) : 0u;
           }
         }
