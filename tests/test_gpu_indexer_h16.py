@@ -281,3 +281,17 @@ def test_few_heads_long_rows(gpu, n1):
         ref = (w[0, t].cpu().unsqueeze(1) * torch.relu(q[0, t].float().cpu() @ kc[:n].T)).sum(0)
         got = logits[0, t, :n].cpu()
         assert float((got - ref).abs().max()) <= 1e-4 * float(ref.abs().max()), f"row {t}"
+
+
+@pytest.mark.parametrize("n1", [1, 32, 33])
+def test_head_tile_boundary(gpu, n1):
+    # head counts at the one-tile / two-tile boundary (N1 <= 32 computes one
+    # 32-head tile): logits against the oracle, indices under the reference rule
+    rng = np.random.RandomState(100 + n1)
+    B, S1, S2, K = 2, 20, 3000, 512
+    print(f"indexer bf16 N1={n1} head-tile boundary", flush=True)
+    q = _rand(rng, (B, S1, n1, 128), torch.bfloat16)
+    k = _rand(rng, (B, S2, 1, 128), torch.bfloat16)
+    w = _rand(rng, (B, S1, n1), torch.bfloat16).abs()
+    _run(gpu, q, k, w, torch.full((B,), S1, dtype=torch.int32), torch.tensor([S2, 2500], dtype=torch.int32), None,
+         "BSND", "BSND", K, 3)
