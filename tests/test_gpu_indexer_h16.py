@@ -258,15 +258,16 @@ def test_paged_long_rows_group_maxima(gpu):
         assert float((got - ref).abs().max()) <= 1e-4 * float(ref.abs().max()), f"row ({b}, {s})"
 
 
-@pytest.mark.parametrize("n1", [8, 24])
-def test_few_heads_long_rows(gpu, n1):
+@pytest.mark.parametrize("n1,S2", [(8, 70000), (24, 70000), (64, 70007)])
+def test_few_heads_long_rows(gpu, n1, S2):
     # N1 <= 32 (the reference examples' head counts) on rows long enough for the
-    # group-maxima top-k: the one-tile kernel with group maxima.  Every row's
+    # group-maxima top-k: the one-tile kernel with group maxima (and 64 heads on a
+    # key count that ends inside a 16-key group).  Every row's
     # indices against the stable sort of the kernel's logits; two rows' logits
     # against the formula.
     from fullsize import check_topk_rows
     g = torch.Generator(device=gpu).manual_seed(n1)
-    S1, S2, K = 24, 70000, 2048
+    S1, K = 24, 2048  # S2 = 70007: the rows' last 16-key group is partial
     print(f"indexer bf16 N1={n1} long rows S2={S2}", flush=True)
     q = torch.randn((1, S1, n1, 128), generator=g, device=gpu).to(torch.bfloat16)
     k = torch.randn((1, S2, 1, 128), generator=g, device=gpu).to(torch.bfloat16)
